@@ -1,0 +1,183 @@
+/* v7g_lib.h -- C ABI of libv7g.so, the MI355X (gfx950) implementation of the
+ * fused per-layer kernels of the v7 inference engine (cpki-gmbh/v7multiplikator).
+ *
+ * Two groups of entry points:
+ *
+ *  1. Drop-in entries with the reference's names, argument order and calling
+ *     convention (V7_ABI = ms_abi on Linux, as src/v7_lib.h:40-46 declares for
+ *     every export of libv7_threading.so).  They take DEVICE pointers and
+ *     enqueue one launch on the library stream; like the reference they return
+ *     nothing and read eps from a library global (the reference's g_rms_eps,
+ *     set here by v7g_set_rms_eps).  Contract violations do not abort: they set
+ *     the sticky error read by v7g_get_last_error().
+ *
+ *  2. Batched v7g_* entries (plain C calling convention) that process many
+ *     rows/tokens per launch -- the performance path.  They return 0 or a
+ *     V7G_ERR_* code (also recorded as the sticky error).
+ *
+ * All data pointers are device pointers (hipMalloc, or torch tensors on
+ * cuda:N).  The library never allocates on a kernel call; v7s_rope_init /
+ * v7g_rope_init are the only entries that allocate (the library-owned
+ * cos/sin tables, as the reference's v7s_rope_init owns its tables).
+ * Launches are asynchronous on the stream set by v7g_set_stream (default: the
+ * null stream); v7g_sync() waits for it.
+ */
+#ifndef V7G_LIB_H
+#define V7G_LIB_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__linux__) && defined(__x86_64__)
+#define V7_ABI __attribute__((ms_abi))
+#else
+#define V7_ABI
+#endif
+
+#define V7G_LIBRARY_NAME "libv7g.so"
+
+/* Error codes (v7g_get_last_error, return values of the batched entries). */
+#define V7G_OK 0
+#define V7G_ERR_NULL 1       /* a required pointer is NULL */
+#define V7G_ERR_SHAPE 2      /* a size violates the kernel contract */
+#define V7G_ERR_ALIGN 3      /* a pointer is not aligned as the kernel needs */
+#define V7G_ERR_HIP 4        /* the HIP runtime reported an error */
+#define V7G_ERR_NO_TABLES 5  /* RoPE tables requested before v7s_rope_init */
+
+/* Q8 tensor descriptor: int8 codes + per-group f32 scales (GS = 64).
+ * Same layout as v7_q8_tensor, src/v7_lib.h:52-56. */
+typedef struct v7g_q8_tensor {
+    char *q;
+    float *s;
+} v7g_q8_tensor;
+
+/* ---------------------------------------------------------------------------
+ * 1. Drop-in entries (reference signatures, device pointers, ms_abi)
+ * ------------------------------------------------------------------------- */
+
+/* Replaces v7s_fused_add_rmsnorm, typedef src/v7_lib.h:272, kernel
+ * src/asm/add_rmsnorm_kernel.inc:15-129.  One row: residual += add (in place),
+ * o = residual * rms_scale * weight.  Contract dim % 8 == 0, dim <= 16384. */
+typedef void(V7_ABI *v7s_fused_add_rmsnorm_fn)(float *o, float *residual, float *add, float *weight, int dim);
+V7_ABI void v7s_fused_add_rmsnorm(float *o, float *residual, float *add, float *weight, int dim);
+
+/* Replaces v7s_rmsnorm_rope_heads, typedef src/v7_lib.h:273, dispatcher
+ * src/asm/rmsnorm_rope_dispatch.inc:11-52.  n_heads heads of one token,
+ * contiguous in buf, normalised and rotated in place at position pos; the
+ * tables hold rope_max_dim floats per position and at least pos+1 rows.
+ * Contract head_dim % 32 == 0, 64 <= head_dim <= 512, rope_max_dim >= head_dim/2. */
+typedef void(V7_ABI *v7s_rmsnorm_rope_heads_fn)(float *buf, int n_heads, int head_dim, float *norm_weight,
+                                                float *cos_table, float *sin_table, int pos, int rope_max_dim);
+V7_ABI void v7s_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, float *norm_weight, float *cos_table,
+                                   float *sin_table, int pos, int rope_max_dim);
+
+/* Replaces v7d_quantize, typedef src/v7_lib.h:123, src/asm/utility_dispatch.inc:108-212:
+ * n floats -> n int8 codes + ceil(n/64) f32 scales, group size 64. */
+typedef void(V7_ABI *v7d_quantize_fn)(char *out_q, float *in_x, float *out_s, int n);
+V7_ABI void v7d_quantize(char *out_q, float *in_x, float *out_s, int n);
+
+/* Replaces the engine-internal v7s_embedding_row(out, token, dim, q_desc),
+ * src/asm/forward.inc:13-42 (no export in src/v7_threading.def; exported here).
+ * out[i] = q[token*dim + i] * s[(token*dim)/64 + i/64].  q_desc is a HOST
+ * struct holding device pointers.  Contract dim % 64 == 0. */
+typedef void(V7_ABI *v7s_embedding_row_fn)(float *out, int token, int dim, v7g_q8_tensor *q_desc);
+V7_ABI void v7s_embedding_row(float *out, int token, int dim, v7g_q8_tensor *q_desc);
+
+/* Elementwise SwiGLU over one row, in place over the gate row as
+ * .pq_ffn_silu does (src/asm/prefill_q8.inc:1154-1168, no reference export). */
+typedef void(V7_ABI *v7s_swiglu_row_fn)(float *gate_inout, float *up, int hidden);
+V7_ABI void v7s_swiglu_row(float *gate_inout, float *up, int hidden);
+
+/* SwiGLU -> Q8 over one row, the chain of src/asm/prefill_q8.inc:1154-1183
+ * (.pq_ffn_silu then v7d_quantize, group size 64), fused into one launch:
+ * out_q[hidden] codes, out_s[ceil(hidden/64)] scales; gate/up are not modified. */
+typedef void(V7_ABI *v7s_swiglu_quantize_row_fn)(char *out_q, float *gate, float *up, float *out_s, int hidden);
+V7_ABI void v7s_swiglu_quantize_row(char *out_q, float *gate, float *up, float *out_s, int hidden);
+
+/* Replaces v7s_rope_init, typedef src/v7_lib.h:275, src/asm/fused_dispatch.inc:58-76:
+ * builds the library-owned device cos/sin tables, [131072, head_dim/2] each
+ * (positions 0..131071, src/asm/fused_f32_kernel.inc:9), freq_j =
+ * base^(-j/(head_dim/2)).  v7g_get_rope_tables returns them. */
+typedef void(V7_ABI *v7s_rope_init_fn)(int head_dim, float rope_base);
+V7_ABI void v7s_rope_init(int head_dim, float rope_base);
+
+/* ---------------------------------------------------------------------------
+ * 2. Library control
+ * ------------------------------------------------------------------------- */
+
+/* Initialises the HIP runtime on the current device (optional: every entry
+ * initialises lazily).  Returns V7G_OK or V7G_ERR_HIP. */
+int v7g_init(void);
+/* Stream for all subsequent launches (a hipStream_t; NULL = null stream). */
+void v7g_set_stream(void *stream);
+void *v7g_get_stream(void);
+/* Waits for the library stream; returns V7G_OK or V7G_ERR_HIP. */
+int v7g_sync(void);
+/* eps used by the drop-in norm entries (the reference's g_rms_eps global,
+ * src/asm/v7_data.inc:509; default 1e-6). */
+void v7g_set_rms_eps(float eps);
+float v7g_get_rms_eps(void);
+/* First error recorded since the last clear (V7G_OK if none). */
+int v7g_get_last_error(void);
+void v7g_clear_last_error(void);
+const char *v7g_error_string(int code);
+/* Library-owned RoPE tables built by v7s_rope_init / v7g_rope_init. */
+int v7g_get_rope_tables(float **cos_table, float **sin_table, int *rope_max_dim, int *n_pos);
+/* As v7s_rope_init with an explicit position count (1 .. 131072). */
+int v7g_rope_init(int head_dim, float rope_base, int n_pos);
+/* Fills caller-owned device tables [n_pos, head_dim/2] (host-built in extended
+ * precision, then copied; synchronous). */
+int v7g_build_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base);
+
+/* ---------------------------------------------------------------------------
+ * 3. Batched entries (performance path)
+ * ------------------------------------------------------------------------- */
+
+/* rows x dim fused add+RMSNorm; rows contiguous (row stride = dim).
+ * residual is updated in place; o may alias residual.  dim % 8 == 0, dim <= 16384,
+ * pointers 16-byte aligned. */
+int v7g_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
+                          float eps);
+
+/* RMSNorm+RoPE over n_tokens tokens of n_heads heads each.  Token t's heads
+ * start at buf + t*token_stride (floats) and are contiguous.  Position of token
+ * t: positions[t] (device int32 array) or, if positions is NULL, pos0 + t.
+ * Tables: table_rows rows of rope_max_dim floats (a position outside the tables
+ * yields NaN heads). */
+int v7g_rmsnorm_rope_heads(float *buf, int n_tokens, long long token_stride, int n_heads, int head_dim,
+                           const float *norm_weight, const float *cos_table, const float *sin_table,
+                           const int32_t *positions, int pos0, int rope_max_dim, int table_rows, float eps);
+
+/* Q and K heads of n_tokens tokens in one launch (the reentrant two-sided form
+ * of v7s_qk_fork_heads, src/asm/qk_fork_kernel.inc:40-62): Q with q_norm_weight,
+ * K with k_norm_weight; q/k may live inside one fused QKV row (strides). */
+int v7g_qk_rmsnorm_rope(float *q, long long q_token_stride, int n_q_heads, const float *q_norm_weight, float *k,
+                        long long k_token_stride, int n_kv_heads, const float *k_norm_weight, int n_tokens,
+                        int head_dim, const float *cos_table, const float *sin_table, const int32_t *positions,
+                        int pos0, int rope_max_dim, int table_rows, float eps);
+
+/* out[i] = (sigmoid(gate[i]) * gate[i]) * up[i] for n elements; out may alias gate. */
+int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n);
+
+/* SwiGLU -> Q8: rows x hidden, group size gs (32 or 64, or any 1..4096 on the
+ * general path); out_q [rows*hidden] int8, out_s [rows, ceil(hidden/gs)] f32. */
+int v7g_swiglu_q8(int8_t *out_q, float *out_s, const float *gate, const float *up, int rows, int hidden, int gs);
+
+/* Q8 block quantization of rows x row_len floats (v7d_quantize per row),
+ * scales [rows, ceil(row_len/gs)]. */
+int v7g_quantize_q8(int8_t *out_q, float *out_s, const float *x, int rows, int row_len, int gs);
+
+/* Q8 embedding gather: out[t, :] = dequant(table row ids[t]) for n_tokens ids
+ * (device int32).  table_q [vocab, dim] int8, table_s [vocab*dim/64] f32.  An id
+ * outside [0, vocab) yields a zero row.  dim % 64 == 0. */
+int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const int8_t *table_q,
+                            const float *table_s, int dim, int vocab);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* V7G_LIB_H */

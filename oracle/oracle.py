@@ -1,0 +1,263 @@
+"""Python bindings of the CPU oracle (test infrastructure only).
+
+Only the test suite, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
+``bench.py`` import this module; the product (``v7multiplikator_amd``) never
+does.  The C restatement lives in ``v7_oracle.c`` (scalar) and
+``v7_oracle_avx2.c`` (AVX2, the CPU baseline); ``make -C oracle`` builds
+``liboracle.so``.
+
+Besides the lane-faithful restatements, this module holds double-precision
+references restating the reference's own C checkers in ``tools/kt_utils.h``
+(``kt_quantize_c_ref`` :378-407, ``v7s_rmsnorm_rope_heads_c_ref`` :460-485,
+``v7s_fused_add_rmsnorm_c_ref`` :493-503) -- the checks the reference's
+validators apply to its NASM kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+
+def lib():
+    """Loads liboracle.so (built by ``make -C oracle``)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"{_LIB_PATH} is missing: run `make -C oracle`")
+        L = ctypes.CDLL(_LIB_PATH)
+        c_int, c_ll, c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_float
+        sig = {
+            "orc_sumsq_lanes": (c_float, [_f32p, c_int]),
+            "orc_rms_scale": (c_float, [c_float, c_int, c_float]),
+            "orc_fused_add_rmsnorm_rows": (None, [_f32p, _f32p, _f32p, _f32p, c_int, c_int, c_float]),
+            "orc_rmsnorm_rope_tokens": (None, [_f32p, c_int, c_ll, c_int, c_int, _f32p, _f32p, _f32p, _i32p, c_int,
+                                               c_float]),
+            "orc_rope_tables": (None, [_f32p, _f32p, c_int, c_int, c_float]),
+            "orc_sigmoid": (c_float, [c_float]),
+            "orc_swiglu": (None, [_f32p, _f32p, _f32p, c_ll]),
+            "orc_quantize_rows": (None, [_i8p, _f32p, _f32p, c_int, c_int, c_int]),
+            "orc_swiglu_q8_rows": (None, [_i8p, _f32p, _f32p, _f32p, c_int, c_int, c_int]),
+            "orc_embedding_gather": (None, [_f32p, _i32p, c_int, c_int, _i8p, _f32p]),
+            "orc_avx2_available": (c_int, []),
+            "orc_avx2_fused_add_rmsnorm": (None, [_f32p, _f32p, _f32p, _f32p, c_int, c_float]),
+            "orc_avx2_rmsnorm_rope_heads": (None, [_f32p, c_int, c_int, _f32p, _f32p, _f32p, c_int, c_int, c_float]),
+            "orc_avx2_swiglu": (None, [_f32p, _f32p, _f32p, c_ll]),
+            "orc_avx2_quantize": (None, [_i8p, _f32p, _f32p, c_ll, c_int]),
+            "orc_avx2_embedding_row": (None, [_f32p, c_int, c_int, _i8p, _f32p]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+# --------------------------------------------------------------------------- lane-faithful oracle
+
+def fused_add_rmsnorm(residual, add, weight, eps):
+    """Returns (o, residual_updated) for rows x dim inputs (copies; inputs untouched)."""
+    r = _c(residual, np.float32).copy()
+    a = _c(add, np.float32)
+    w = _c(weight, np.float32)
+    rows, dim = r.reshape(-1, r.shape[-1]).shape
+    o = np.empty_like(r)
+    lib().orc_fused_add_rmsnorm_rows(o, r, a, w, rows, dim, eps)
+    return o, r
+
+
+def sumsq_lanes(x):
+    x = _c(x, np.float32)
+    return np.float32(lib().orc_sumsq_lanes(x, x.size))
+
+
+def rms_scale(ss, n, eps):
+    return np.float32(lib().orc_rms_scale(float(ss), int(n), float(eps)))
+
+
+def rmsnorm_rope(buf, norm_weight, cos_table, sin_table, positions, eps):
+    """buf [T, H, D] -> new array; positions [T] int32; tables [P, rope_max_dim]."""
+    b = _c(buf, np.float32).copy()
+    T, H, D = b.shape
+    ct = _c(cos_table, np.float32)
+    st = _c(sin_table, np.float32)
+    pos = _c(positions, np.int32)
+    lib().orc_rmsnorm_rope_tokens(b, T, H * D, H, D, _c(norm_weight, np.float32), ct, st, pos, ct.shape[-1], eps)
+    return b
+
+
+def rope_tables(n_pos, head_dim, base):
+    half = head_dim // 2
+    c = np.empty((n_pos, half), np.float32)
+    s = np.empty((n_pos, half), np.float32)
+    lib().orc_rope_tables(c, s, n_pos, head_dim, float(base))
+    return c, s
+
+
+def sigmoid(g):
+    return np.float32(lib().orc_sigmoid(float(g)))
+
+
+def swiglu(gate, up):
+    g = _c(gate, np.float32)
+    u = _c(up, np.float32)
+    out = np.empty_like(g)
+    lib().orc_swiglu(out, g, u, g.size)
+    return out
+
+
+def quantize(x, gs, row_len=None):
+    """x [rows, row_len] (or flat with row_len) -> (codes int8 same shape, scales [rows, ceil(row_len/gs)])."""
+    x = _c(x, np.float32)
+    if row_len is None:
+        row_len = x.shape[-1]
+    rows = x.size // row_len
+    spr = -(-row_len // gs)
+    q = np.empty(x.size, np.int8)
+    s = np.empty(rows * spr, np.float32)
+    lib().orc_quantize_rows(q, x.reshape(-1), s, rows, row_len, gs)
+    return q.reshape(x.shape), s.reshape(rows, spr)
+
+
+def swiglu_q8(gate, up, gs):
+    g = _c(gate, np.float32)
+    u = _c(up, np.float32)
+    hidden = g.shape[-1]
+    rows = g.size // hidden
+    spr = -(-hidden // gs)
+    q = np.empty(g.size, np.int8)
+    s = np.empty(rows * spr, np.float32)
+    lib().orc_swiglu_q8_rows(q, s, g.reshape(-1), u.reshape(-1), rows, hidden, gs)
+    return q.reshape(g.shape), s.reshape(rows, spr)
+
+
+def embedding_gather(ids, table_q, table_s, dim):
+    ids = _c(ids, np.int32)
+    out = np.empty((ids.size, dim), np.float32)
+    lib().orc_embedding_gather(out, ids, ids.size, dim, _c(table_q, np.int8).reshape(-1),
+                               _c(table_s, np.float32).reshape(-1))
+    return out
+
+
+# --------------------------------------------------------------------------- AVX2 restatement (CPU baseline)
+
+def avx2_available():
+    return bool(lib().orc_avx2_available())
+
+
+def avx2_fused_add_rmsnorm_rows(residual, add, weight, eps):
+    r = _c(residual, np.float32).copy()
+    a = _c(add, np.float32)
+    w = _c(weight, np.float32)
+    o = np.empty_like(r)
+    dim = r.shape[-1]
+    for i in range(r.size // dim):
+        ro, ao, oo = r.reshape(-1, dim)[i], a.reshape(-1, dim)[i], o.reshape(-1, dim)[i]
+        lib().orc_avx2_fused_add_rmsnorm(oo, ro, ao, w, dim, eps)
+    return o, r
+
+
+def avx2_rmsnorm_rope(buf, norm_weight, cos_table, sin_table, positions, eps):
+    b = _c(buf, np.float32).copy()
+    T, H, D = b.shape
+    ct = _c(cos_table, np.float32)
+    st = _c(sin_table, np.float32)
+    w = _c(norm_weight, np.float32)
+    for t in range(T):
+        lib().orc_avx2_rmsnorm_rope_heads(b[t], H, D, w, ct, st, int(positions[t]), ct.shape[-1], eps)
+    return b
+
+
+def avx2_swiglu(gate, up):
+    g = _c(gate, np.float32)
+    u = _c(up, np.float32)
+    out = np.empty_like(g)
+    lib().orc_avx2_swiglu(out, g, u, g.size)
+    return out
+
+
+def avx2_quantize(x, gs):
+    x = _c(x, np.float32)
+    row_len = x.shape[-1]
+    rows = x.size // row_len
+    spr = -(-row_len // gs)
+    q = np.empty((rows, row_len), np.int8)
+    s = np.empty((rows, spr), np.float32)
+    xr = x.reshape(rows, row_len)
+    for r in range(rows):
+        lib().orc_avx2_quantize(q[r], xr[r], s[r], row_len, gs)
+    return q.reshape(x.shape), s
+
+
+def avx2_embedding_gather(ids, table_q, table_s, dim):
+    ids = _c(ids, np.int32)
+    out = np.empty((ids.size, dim), np.float32)
+    tq = _c(table_q, np.int8).reshape(-1)
+    ts = _c(table_s, np.float32).reshape(-1)
+    for t in range(ids.size):
+        lib().orc_avx2_embedding_row(out[t], int(ids[t]), dim, tq, ts)
+    return out
+
+
+# --------------------------------------------------------------------------- reference C checkers, restated
+
+def kt_quantize_c_ref(x):
+    """tools/kt_utils.h:378-407 (GS 64, float arithmetic, lrintf, all-zero scale 1/127)."""
+    x = _c(x, np.float32).reshape(-1)
+    n = x.size
+    gs = 64
+    ng = -(-n // gs)
+    q = np.empty(n, np.int8)
+    s = np.empty(ng, np.float32)
+    for g in range(ng):
+        seg = x[g * gs:(g + 1) * gs]
+        wmax = np.float32(np.max(np.abs(seg))) if seg.size else np.float32(0)
+        scale = np.float32(1.0) / np.float32(127.0) if wmax == 0 else wmax / np.float32(127.0)
+        s[g] = scale
+        recip = np.float32(1.0) / np.float32(scale)
+        val = seg * recip
+        qi = np.rint(val).astype(np.int64)
+        q[g * gs:g * gs + seg.size] = np.clip(qi, -127, 127).astype(np.int8)
+    return q, s
+
+
+def kt_fused_add_rmsnorm_c_ref(residual, add, weight, eps):
+    """tools/kt_utils.h:493-503, float accumulation in element order."""
+    r = (_c(residual, np.float32) + _c(add, np.float32)).astype(np.float32)
+    ss = np.float32(0)
+    for v in r:
+        ss = np.float32(ss + np.float32(v * v))
+    scale = np.float32(1.0) / np.sqrt(np.float32(ss / np.float32(r.size) + np.float32(eps)))
+    return (r * scale * _c(weight, np.float32)).astype(np.float32), r
+
+
+def rmsnorm_rope_double_ref(buf, norm_weight, cos_table, sin_table, positions, eps):
+    """tools/kt_utils.h:460-485 vectorised: double sum of squares and rotation, per head."""
+    b = np.asarray(buf, np.float64)
+    T, H, D = b.shape
+    half = D // 2
+    ss = np.sum(b * b, axis=-1, keepdims=True)
+    scale = 1.0 / np.sqrt(ss / D + float(eps))
+    qn = (b * np.asarray(norm_weight, np.float64) * scale).astype(np.float32).astype(np.float64)
+    pos = np.asarray(positions)
+    c = np.asarray(cos_table, np.float64)[pos][:, None, :half]
+    s = np.asarray(sin_table, np.float64)[pos][:, None, :half]
+    x0, y0 = qn[..., :half], qn[..., half:]
+    out = np.empty_like(qn)
+    out[..., :half] = x0 * c - y0 * s
+    out[..., half:] = x0 * s + y0 * c
+    return out.astype(np.float32)

@@ -1,0 +1,351 @@
+/* v7_oracle.c -- scalar CPU oracle for v7's fused per-layer kernels.
+ *
+ * TEST INFRASTRUCTURE ONLY.  The test suite, the smoke check and the
+ * benchmark's CPU-baseline leg are the only users; the product (the HIP
+ * library) never links or calls it.
+ *
+ * Each function restates one NASM kernel of the reference engine,
+ * cpki-gmbh/v7multiplikator, in plain C.  The restatement follows the
+ * reference instruction by instruction wherever the order of floating-point
+ * operations is observable:
+ *   - every vaddps/vmulps/vdivps/vsqrtps is one correctly rounded C operator,
+ *   - every vfmadd/vfnmadd is one fmaf() call,
+ *   - the eight-lane YMM accumulators are modelled as explicit arrays and
+ *     reduced by the same addition tree as the reference's HADD_YMM macro.
+ * Compile with -ffp-contract=off and without -ffast-math (see Makefile).
+ *
+ * Parity pins (what fixes each function besides this restatement) are listed
+ * in the test suite: tests/test_oracle.py.
+ */
+#include "v7_oracle.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* HADD_YMM: src/asm/v7_macros.inc:38-45.  v[i] + v[i+4] for i < 4, then
+ * (s0 + s1) + (s2 + s3): vmovshdup pairs lanes 0/1 and 2/3, vmovhlps brings
+ * lane 2 down to lane 0. */
+static float hadd8(const float v[8])
+{
+    float s0 = v[0] + v[4];
+    float s1 = v[1] + v[5];
+    float s2 = v[2] + v[6];
+    float s3 = v[3] + v[7];
+    float t0 = s0 + s1;
+    float t2 = s2 + s3;
+    return t0 + t2;
+}
+
+/* Sum of squares with four YMM accumulators A..D.
+ * src/asm/add_rmsnorm_kernel.inc:29-73 (Pass 1 + reduce) and
+ * src/asm/v7_macros.inc:263-291 (RMSNORM_ROPE_BODY Pass 1).
+ * The row is split into 8-float blocks.  Blocks that do not fill a 4-way group
+ * (blocks % 4) are accumulated first, all into A (add_rmsnorm_kernel.inc:37-39,
+ * 112-121); then each group of four blocks feeds A, B, C, D in turn
+ * (add_rmsnorm_kernel.inc:45-68).  For n % 32 == 0 this is exactly the
+ * RMSNORM_ROPE_BODY loop, whose 32-element block feeds elements 0-7 to A, 8-15
+ * to B, 16-23 to C and 24-31 to D.  Reduction: (A+B) + (C+D) lane-wise, then
+ * HADD_YMM (add_rmsnorm_kernel.inc:70-73, v7_macros.inc:286-289). */
+float orc_sumsq_lanes(const float *x, int n)
+{
+    float acc[4][8];
+    memset(acc, 0, sizeof(acc));
+    int blocks = n / 8;
+    int left = blocks & 3;
+    int b = 0;
+    for (; b < left; ++b)
+        for (int j = 0; j < 8; ++j)
+            acc[0][j] = fmaf(x[8 * b + j], x[8 * b + j], acc[0][j]);
+    for (int g = 0; g < blocks / 4; ++g)
+        for (int q = 0; q < 4; ++q, ++b)
+            for (int j = 0; j < 8; ++j)
+                acc[q][j] = fmaf(x[8 * b + j], x[8 * b + j], acc[q][j]);
+    float v[8];
+    for (int j = 0; j < 8; ++j) {
+        float ab = acc[0][j] + acc[1][j];
+        float cd = acc[2][j] + acc[3][j];
+        v[j] = ab + cd;
+    }
+    return hadd8(v);
+}
+
+/* COMPUTE_RMS_SCALE: src/asm/v7_macros.inc:348-354.
+ * vdivss sumsq/dim; vaddss eps (g_rms_eps); vsqrtss; vdivss 1/x.  dim is
+ * converted with vcvtsi2ss (add_rmsnorm_kernel.inc:74-75,
+ * rmsnorm_rope_dispatch.inc:20). */
+float orc_rms_scale(float sumsq, int n, float eps)
+{
+    float mean = sumsq / (float)n;
+    float val = mean + eps;
+    float root = sqrtf(val);
+    return 1.0f / root;
+}
+
+/* v7s_fused_add_rmsnorm(o, residual, add, weight, dim):
+ * src/asm/add_rmsnorm_kernel.inc:15-129, typedef src/v7_lib.h:272.
+ * Pass 1: residual = residual + add (vaddps, stored in place).
+ * Pass 2: o = (scale * residual) * weight, two vmulps (:87-94). */
+void orc_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int dim, float eps)
+{
+    for (int i = 0; i < dim; ++i)
+        residual[i] = residual[i] + add[i];
+    float ss = orc_sumsq_lanes(residual, dim);
+    float s = orc_rms_scale(ss, dim, eps);
+    for (int i = 0; i < dim; ++i) {
+        float t = s * residual[i];
+        o[i] = t * weight[i];
+    }
+}
+
+void orc_fused_add_rmsnorm_rows(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
+                                float eps)
+{
+    for (int r = 0; r < rows; ++r)
+        orc_fused_add_rmsnorm(o + (long long)r * dim, residual + (long long)r * dim, add + (long long)r * dim, weight,
+                              dim, eps);
+}
+
+/* One head of v7s_rmsnorm_rope_heads: RMSNORM_ROPE_BODY,
+ * src/asm/v7_macros.inc:263-340, driven by rmsnorm_rope_kernel.inc:7-23
+ * (and identically by qk_fork_kernel.inc:40-62).  cos/sin point at the row of
+ * this position already (rmsnorm_rope_dispatch.inc:24-33). */
+static void rope_head(float *x, int head_dim, const float *w, const float *c, const float *s, int pos, float eps)
+{
+    float ss = orc_sumsq_lanes(x, head_dim);
+    float scale = orc_rms_scale(ss, head_dim, eps);
+    if (pos == 0) {
+        /* %%rmsnorm_only, v7_macros.inc:325-339 */
+        for (int i = 0; i < head_dim; ++i) {
+            float t = x[i] * scale;
+            x[i] = t * w[i];
+        }
+        return;
+    }
+    /* %%rp_loop, v7_macros.inc:305-323 */
+    int half = head_dim / 2;
+    for (int j = 0; j < half; ++j) {
+        float xe = x[j] * scale;
+        float xo = x[j + half] * scale;
+        xe = xe * w[j];
+        xo = xo * w[j + half];
+        float re = xe * c[j];
+        float ro = xe * s[j];
+        re = fmaf(-xo, s[j], re); /* vfnmadd231ps: re - xo*sin, one rounding */
+        ro = fmaf(xo, c[j], ro);  /* vfmadd231ps: ro + xo*cos, one rounding */
+        x[j] = re;
+        x[j + half] = ro;
+    }
+}
+
+/* v7s_rmsnorm_rope_heads(buf, n_heads, head_dim, norm_weight, cos, sin, pos,
+ * rope_max_dim): src/asm/rmsnorm_rope_dispatch.inc:11-52; typedef
+ * src/v7_lib.h:273.  One job per head, heads contiguous in buf; eps is the
+ * g_rms_eps global in the reference and an argument here. */
+void orc_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, const float *norm_weight, const float *cos_table,
+                            const float *sin_table, int pos, int rope_max_dim, float eps)
+{
+    const float *c = cos_table + (long long)pos * rope_max_dim;
+    const float *s = sin_table + (long long)pos * rope_max_dim;
+    for (int h = 0; h < n_heads; ++h)
+        rope_head(buf + (long long)h * head_dim, head_dim, norm_weight, c, s, pos, eps);
+}
+
+void orc_rmsnorm_rope_tokens(float *buf, int n_tokens, long long token_stride, int n_heads, int head_dim,
+                             const float *norm_weight, const float *cos_table, const float *sin_table,
+                             const int32_t *positions, int rope_max_dim, float eps)
+{
+    for (int t = 0; t < n_tokens; ++t)
+        orc_rmsnorm_rope_heads(buf + (long long)t * token_stride, n_heads, head_dim, norm_weight, cos_table, sin_table,
+                               positions[t], rope_max_dim, eps);
+}
+
+/* RoPE tables: src/asm/fused_f32_kernel.inc:69-147,257-303 (plain, type 0).
+ * freq_j = base^(-j/half) computed in x87 extended precision and stored as a
+ * double; angle = freq_j * pos in extended precision; cos/sin by fsincos,
+ * rounded to float on store.  Restated with long double powl/cosl/sinl.  The
+ * tables are inputs to the kernels, identical on both sides of every parity
+ * check, so they need no bit parity with the x87 sequence. */
+void orc_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base)
+{
+    int half = head_dim / 2;
+    double freq[512];
+    for (int j = 0; j < half; ++j)
+        freq[j] = (double)powl((long double)rope_base, -(long double)j / (long double)half);
+    for (int p = 0; p < n_pos; ++p) {
+        for (int j = 0; j < half; ++j) {
+            long double a = (long double)freq[j] * (long double)p;
+            cos_table[(long long)p * half + j] = (float)cosl(a);
+            sin_table[(long long)p * half + j] = (float)sinl(a);
+        }
+    }
+}
+
+/* EVAL_SIGMOID, packed form: src/asm/v7_macros.inc:98-160; constants
+ * src/asm/math_data.inc:16-53. */
+static float bits_to_float(uint32_t u)
+{
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+float orc_sigmoid(float g)
+{
+    const float log2e = (float)1.4426950408889634; /* scalar_log2e / s_log2e_v */
+    const float c5 = bits_to_float(0x3AADD303u);
+    const float c4 = bits_to_float(0x3C1E7411u);
+    const float c3 = bits_to_float(0x3D635B9Bu);
+    const float c2 = bits_to_float(0x3E75FCE0u);
+    const float c1 = bits_to_float(0x3F317215u);
+    float x = -g;                       /* vxorps sign mask */
+    x = (x > -80.0f) ? x : -80.0f;      /* vmaxps x, -80: src1 > src2 ? src1 : src2 */
+    x = (x < 80.0f) ? x : 80.0f;        /* vminps x, 80: src1 < src2 ? src1 : src2 */
+    float fx = x * log2e;               /* vmulps */
+    float ip = nearbyintf(fx);          /* vroundps imm 0: nearest-even */
+    float fp = fx - ip;                 /* vsubps */
+    int32_t ii = (int32_t)ip;           /* vcvttps2dq, ip is already integral */
+    float p2 = bits_to_float((uint32_t)(ii + 127) << 23); /* vpaddd bias, vpslld 23 */
+    float p = c5;                       /* vbroadcastss C5 */
+    p = fmaf(fp, p, c4);                /* vfmadd213ps: fpart*acc + C4 */
+    p = fmaf(fp, p, c3);
+    p = fmaf(fp, p, c2);
+    p = fmaf(fp, p, c1);
+    p = fmaf(fp, p, 1.0f);
+    float e = p2 * p;                   /* vmulps ymm0, ymm5, ymm4 */
+    float d = e + 1.0f;                 /* vaddps */
+    return 1.0f / d;                    /* vdivps */
+}
+
+/* Elementwise SwiGLU, the .pq_ffn_silu loop: src/asm/prefill_q8.inc:1159-1166.
+ * out = (sigmoid(g) * g) * u, two vmulps. */
+void orc_swiglu(float *out, const float *gate, const float *up, long long n)
+{
+    for (long long i = 0; i < n; ++i) {
+        float g = gate[i];
+        float sg = orc_sigmoid(g) * g;
+        out[i] = sg * up[i];
+    }
+}
+
+/* v7d_quantize / v7s_quantize_chunk: src/asm/utility_dispatch.inc:108-212,
+ * src/asm/quantize_kernel.inc:44-159; typedef src/v7_lib.h:123.
+ * The reference group size is GS = 64 (src/asm/v7_core.inc:120); gs is a
+ * parameter here so the same algorithm also covers 32-element blocks. */
+static const float Q_FLOOR = 1.4928778e-36f; /* scalar_epsilon, quantize_kernel.inc:40-41: 127 * 2^-126 */
+
+/* Full-group code: vmulps, vcvtps2dq (nearest-even; NaN and out-of-range give
+ * 0x80000000), vpackssdw + vpacksswb (signed saturation), vpmaxsb -127
+ * (quantize_kernel.inc:91-105). */
+static int8_t code_vec(float v)
+{
+    int32_t i;
+    if (!(v >= -2147483648.0f && v < 2147483648.0f))
+        i = INT32_MIN;
+    else
+        i = (int32_t)nearbyintf(v);
+    if (i < -128)
+        i = -128;
+    if (i > 127)
+        i = 127;
+    if (i < -127)
+        i = -127;
+    return (int8_t)i;
+}
+
+/* Tail code: vmaxss -127 (NaN gives -127), vminss 127, vcvtss2si
+ * (quantize_kernel.inc:143-149). */
+static int8_t code_tail(float v)
+{
+    v = (v > -127.0f) ? v : -127.0f;
+    v = (v < 127.0f) ? v : 127.0f;
+    return (int8_t)(int32_t)nearbyintf(v);
+}
+
+static float absf_bits(float v)
+{
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    u &= 0x7FFFFFFFu; /* vandps abs mask */
+    return bits_to_float(u);
+}
+
+void orc_quantize(int8_t *out_q, const float *in_x, float *out_s, long long n, int gs)
+{
+    long long full = n / gs;
+    for (long long g = 0; g < full; ++g) {
+        const float *x = in_x + g * gs;
+        /* absmax: vandps + vmaxps tree (:62-83); max is order-free on non-NaN input */
+        float wmax = absf_bits(x[0]);
+        for (int i = 1; i < gs; ++i) {
+            float a = absf_bits(x[i]);
+            wmax = (wmax > a) ? wmax : a;
+        }
+        wmax = (wmax > Q_FLOOR) ? wmax : Q_FLOOR; /* vmaxss wmax, eps (:84) */
+        float scale = wmax / 127.0f;              /* vdivss (:86) */
+        out_s[g] = scale;
+        float recip = 1.0f / scale;               /* vdivss (:88) */
+        for (int i = 0; i < gs; ++i)
+            out_q[g * gs + i] = code_vec(x[i] * recip);
+    }
+    long long rem = n - full * gs;
+    if (rem > 0) {
+        /* scalar tail, quantize_kernel.inc:119-152 */
+        const float *x = in_x + full * gs;
+        float wmax = 0.0f;
+        for (long long i = 0; i < rem; ++i) {
+            float a = absf_bits(x[i]);
+            wmax = (a > wmax) ? a : wmax; /* vmaxss xmm3, |x|, xmm3 */
+        }
+        wmax = (wmax > Q_FLOOR) ? wmax : Q_FLOOR;
+        float scale = wmax / 127.0f;
+        out_s[full] = scale;
+        float recip = 1.0f / scale;
+        for (long long i = 0; i < rem; ++i)
+            out_q[full * gs + i] = code_tail(x[i] * recip);
+    }
+}
+
+void orc_quantize_rows(int8_t *out_q, const float *in_x, float *out_s, int rows, int row_len, int gs)
+{
+    int spr = (row_len + gs - 1) / gs;
+    for (int r = 0; r < rows; ++r)
+        orc_quantize(out_q + (long long)r * row_len, in_x + (long long)r * row_len, out_s + (long long)r * spr, row_len,
+                     gs);
+}
+
+/* SwiGLU -> Q8 per row: src/asm/prefill_q8.inc:1154-1183 (.pq_ffn_silu over the
+ * row, then v7d_quantize over the same row with n = hidden_dim). */
+void orc_swiglu_q8_rows(int8_t *out_q, float *out_s, const float *gate, const float *up, int rows, int hidden, int gs)
+{
+    float *buf = (float *)malloc((size_t)hidden * sizeof(float));
+    if (!buf)
+        return;
+    int spr = (hidden + gs - 1) / gs;
+    for (int r = 0; r < rows; ++r) {
+        orc_swiglu(buf, gate + (long long)r * hidden, up + (long long)r * hidden, hidden);
+        orc_quantize(out_q + (long long)r * hidden, buf, out_s + (long long)r * spr, hidden, gs);
+    }
+    free(buf);
+}
+
+/* v7s_embedding_row(out, token, dim, q_desc): src/asm/forward.inc:13-42.
+ * out[i] = (float)q[token*dim + i] * s[(token*dim >> 6) + i/64]: vpmovsxbd +
+ * vcvtdq2ps (exact) then one vmulps. */
+void orc_embedding_row(float *out, int token, int dim, const int8_t *table_q, const float *table_s)
+{
+    long long base = (long long)token * dim;
+    const int8_t *q = table_q + base;
+    const float *s = table_s + (base >> 6);
+    for (int i = 0; i < dim; ++i)
+        out[i] = (float)q[i] * s[i >> 6];
+}
+
+void orc_embedding_gather(float *out, const int32_t *ids, int n_tokens, int dim, const int8_t *table_q,
+                          const float *table_s)
+{
+    for (int t = 0; t < n_tokens; ++t)
+        orc_embedding_row(out + (long long)t * dim, ids[t], dim, table_q, table_s);
+}

@@ -1,0 +1,102 @@
+/* v7_oracle.h -- CPU oracle for the fused per-layer kernels (TEST INFRASTRUCTURE).
+ *
+ * This is the checker, not the product: only the test suite, the smoke check
+ * and the CPU-baseline leg of the benchmark load it.  The product path is the
+ * HIP library under v7multiplikator_amd/csrc and never calls into this code.
+ *
+ * Every function restates one reference kernel of cpki-gmbh/v7multiplikator
+ * in scalar C, reproducing its operation order, rounding points and FMA
+ * placement (see the per-function citations in v7_oracle.c).  Build flags:
+ * -O2 -ffp-contract=off, no fast-math, so every C operator is one IEEE-754
+ * binary32 operation rounded to nearest-even and fmaf() is the only fused op.
+ */
+#ifndef V7_ORACLE_H
+#define V7_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* a1: v7s_fused_add_rmsnorm, one row; dim % 8 == 0 */
+void orc_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int dim, float eps);
+/* a1 batched: rows x dim, contiguous rows */
+void orc_fused_add_rmsnorm_rows(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
+                                float eps);
+/* a1/a3 building block: the lane-ordered sum of squares of x[0..n), n % 8 == 0 */
+float orc_sumsq_lanes(const float *x, int n);
+/* a2: COMPUTE_RMS_SCALE */
+float orc_rms_scale(float sumsq, int n, float eps);
+
+/* a3: v7s_rmsnorm_rope_heads, one token; tables are the table bases (not pre-offset) */
+void orc_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, const float *norm_weight, const float *cos_table,
+                            const float *sin_table, int pos, int rope_max_dim, float eps);
+/* a3 batched: tokens x heads; token t at buf + t*token_stride, position positions[t] */
+void orc_rmsnorm_rope_tokens(float *buf, int n_tokens, long long token_stride, int n_heads, int head_dim,
+                             const float *norm_weight, const float *cos_table, const float *sin_table,
+                             const int32_t *positions, int rope_max_dim, float eps);
+
+/* a4: RoPE table builder (host, extended precision); tables are [n_pos, half] */
+void orc_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base);
+
+/* a5: EVAL_SIGMOID, ps form */
+float orc_sigmoid(float g);
+/* a6: elementwise SwiGLU (out may alias gate) */
+void orc_swiglu(float *out, const float *gate, const float *up, long long n);
+
+/* a7: v7d_quantize with group size gs (the reference fixes gs = 64); n may leave a partial tail group */
+void orc_quantize(int8_t *out_q, const float *in_x, float *out_s, long long n, int gs);
+/* a7 per row: rows x row_len, scales [rows, ceil(row_len/gs)] */
+void orc_quantize_rows(int8_t *out_q, const float *in_x, float *out_s, int rows, int row_len, int gs);
+/* a8: SwiGLU -> Q8 chain, rows x hidden */
+void orc_swiglu_q8_rows(int8_t *out_q, float *out_s, const float *gate, const float *up, int rows, int hidden, int gs);
+
+/* a9: v7s_embedding_row; scales use 64-element groups over the flat table */
+void orc_embedding_row(float *out, int token, int dim, const int8_t *table_q, const float *table_s);
+void orc_embedding_gather(float *out, const int32_t *ids, int n_tokens, int dim, const int8_t *table_q,
+                          const float *table_s);
+
+/* AVX2 restatement (v7_oracle_avx2.c): same results bit for bit, used as the CPU baseline */
+int orc_avx2_available(void);
+void orc_avx2_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int dim, float eps);
+void orc_avx2_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, const float *norm_weight,
+                                 const float *cos_table, const float *sin_table, int pos, int rope_max_dim, float eps);
+void orc_avx2_swiglu(float *out, const float *gate, const float *up, long long n);
+void orc_avx2_quantize(int8_t *out_q, const float *in_x, float *out_s, long long n, int gs);
+void orc_avx2_embedding_row(float *out, int token, int dim, const int8_t *table_q, const float *table_s);
+
+/* Buffers of the per-layer chain (embedding gather, add+RMSNorm, Q/K RMSNorm+RoPE, SwiGLU -> Q8) over
+ * n_tokens rows, all host memory, rows contiguous. */
+typedef struct orc_chain_args {
+    int n_tokens, dim, n_q_heads, n_kv_heads, head_dim, rope_max_dim, hidden, gs;
+    float eps;
+    const int32_t *ids;
+    const int32_t *positions;
+    const int8_t *table_q;
+    const float *table_s;
+    float *emb_out;
+    float *residual;
+    const float *add;
+    const float *w_norm;
+    float *normed;
+    float *q;
+    float *k;
+    const float *q_w;
+    const float *k_w;
+    const float *cos_table;
+    const float *sin_table;
+    const float *gate;
+    const float *up;
+    float *act;
+    int8_t *codes;
+    float *scales;
+} orc_chain_args;
+
+/* Runs the chain `reps` times, one call per token row as the reference engine does, rows split over
+ * n_threads host threads.  Returns wall seconds. */
+double orc_avx2_chain_bench(const orc_chain_args *a, int n_threads, int reps);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

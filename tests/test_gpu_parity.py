@@ -1,0 +1,303 @@
+"""GPU parity: every kernel of libv7g.so against the CPU oracle on the same seeded inputs.
+
+The bar is bit-exactness for every kernel: the oracle restates the reference
+NASM kernels operation by operation, and the gfx950 kernels reproduce the same
+operation order, so f32 outputs, int8 codes and scales compare with
+np.array_equal (NaN positions compared as NaN).  The tolerances the
+benchmark configurations allow (1e-5 relative for f32, +-1 code on 0.01% of
+elements) are therefore not needed; the benchmark-size cases also report them.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests import common as C
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a visible MI355X")
+    from v7multiplikator_amd import ops as _ops
+    from v7multiplikator_amd import _lib
+    _lib.load()
+    return _ops
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def assert_bits(got, want, what=""):
+    got = np.asarray(got)
+    want = np.asarray(want)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    if got.dtype.kind == "f":
+        same = (got == want) | (np.isnan(got) & np.isnan(want))
+        # +0/-0 must match too
+        same &= np.signbit(got) == np.signbit(want)
+    else:
+        same = got == want
+    if not same.all():
+        idx = np.argwhere(~same)[:5]
+        raise AssertionError(f"{what}: {np.count_nonzero(~same)} of {got.size} differ; first {idx.tolist()} "
+                             f"got {got[tuple(idx[0])]!r} want {want[tuple(idx[0])]!r}")
+
+
+# --------------------------------------------------------------------------- embedding gather (a9)
+
+@pytest.mark.parametrize("vocab,dim,n", [(1000, 64, 7), (512, 128, 33), (3000, 1024, 100), (4096, 4096, 257)])
+def test_embedding_gather_matches_oracle(ops, oracle, vocab, dim, n):
+    tq, ts = C.q8_table(11, vocab, dim)
+    ids = C.rng(12).integers(0, vocab, n).astype(np.int32)
+    want = oracle.embedding_gather(ids, tq, ts, dim)
+    got = ops.embedding_gather_q8(dev(ids), dev(tq), dev(ts))
+    assert_bits(host(got), want, "embedding")
+
+
+def test_embedding_invalid_ids_give_zero_rows(ops, oracle):
+    tq, ts = C.q8_table(3, 64, 128)
+    ids = np.array([0, -1, 63, 64, 1 << 30, 5], np.int32)
+    got = host(ops.embedding_gather_q8(dev(ids), dev(tq), dev(ts)))
+    valid = np.array([0, 63, 5])
+    want = oracle.embedding_gather(valid, tq, ts, 128)
+    assert_bits(got[[0, 2, 5]], want, "valid rows")
+    assert not got[[1, 3, 4]].any()
+
+
+def test_embedding_empty(ops):
+    tq, ts = C.q8_table(3, 16, 64)
+    out = ops.embedding_gather_q8(torch.empty(0, dtype=torch.int32, device="cuda"), dev(tq), dev(ts))
+    assert out.shape == (0, 64)
+
+
+# --------------------------------------------------------------------------- fused add + RMSNorm (a1)
+
+# The reference validator's sizes, tools/v_rmsnorm_validate.cpp:87-101, incl. leftover-block shapes.
+@pytest.mark.parametrize("dim", [8, 16, 24, 48, 64, 128, 256, 1024, 2048, 3072, 8192, 40, 72, 16384])
+@pytest.mark.parametrize("seed", [12345, 67890])
+def test_fused_add_rmsnorm_validator_shapes(ops, oracle, dim, seed):
+    rows = 5
+    r = C.validator_row(seed, rows * dim).reshape(rows, dim)
+    a = C.validator_row(seed + 1, rows * dim).reshape(rows, dim)
+    w = C.validator_weight(seed + 2, dim)
+    for eps in (1e-6, 1e-5):
+        want_o, want_r = oracle.fused_add_rmsnorm(r, a, w, eps)
+        rt = dev(r)
+        got_o = ops.fused_add_rmsnorm(rt, dev(a), dev(w), eps=eps)
+        assert_bits(host(rt), want_r, "residual")
+        assert_bits(host(got_o), want_o, "o")
+
+
+def test_fused_add_rmsnorm_out_aliases_residual(ops, oracle):
+    r = C.normal(5, (64, 2048))
+    a = C.normal(6, (64, 2048))
+    w = C.norm_weight(7, 2048)
+    want_o, _ = oracle.fused_add_rmsnorm(r, a, w, 1e-6)
+    rt = dev(r)
+    ops.fused_add_rmsnorm(rt, dev(a), dev(w), eps=1e-6, out=rt)
+    assert_bits(host(rt), want_o, "in-place o")
+
+
+def test_fused_add_rmsnorm_config1(ops, oracle):
+    """[512, 2048], x/residual ~N(0,1), w = 1+N(0,0.1), eps 1e-6."""
+    r = C.normal(101, (512, 2048))
+    a = C.normal(102, (512, 2048))
+    w = C.norm_weight(103, 2048)
+    want_o, want_r = oracle.fused_add_rmsnorm(r, a, w, 1e-6)
+    rt = dev(r)
+    got = ops.fused_add_rmsnorm(rt, dev(a), dev(w), eps=1e-6)
+    assert_bits(host(rt), want_r, "residual")
+    assert_bits(host(got), want_o, "o")
+
+
+def test_fused_add_rmsnorm_empty(ops):
+    w = torch.ones(64, device="cuda")
+    r = torch.empty((0, 64), device="cuda")
+    assert ops.fused_add_rmsnorm(r, r.clone(), w).shape == (0, 64)
+
+
+# --------------------------------------------------------------------------- RMSNorm + RoPE (a3)
+
+# tools/v_rmsnorm_validate.cpp:67-83: (heads, head_dim, pos, eps), tables theta 1e4, rope_max_dim = head_dim.
+ROPE_VALIDATOR = [(1, 64, 0, 1e-6), (1, 64, 7, 1e-6), (4, 64, 0, 1e-6), (4, 64, 31, 1e-6), (8, 64, 7, 1e-6),
+                  (8, 128, 0, 1e-6), (16, 64, 0, 1e-6), (16, 64, 31, 1e-6), (32, 64, 7, 1e-6), (32, 128, 0, 1e-6),
+                  (40, 64, 31, 1e-6), (40, 128, 7, 1e-6), (32, 64, 0, 1e-5), (32, 64, 31, 1e-5), (8, 64, 7, 1e-5)]
+
+
+@pytest.mark.parametrize("heads,hd,pos,eps", ROPE_VALIDATOR)
+@pytest.mark.parametrize("seed", [12345, 67890])
+def test_rmsnorm_rope_validator_cases(ops, oracle, heads, hd, pos, eps, seed):
+    buf = C.validator_row(seed, heads * hd).reshape(1, heads, hd)
+    w = C.validator_weight(seed + 1, hd)
+    ct, st = C.validator_rope_tables(pos, hd, hd)
+    want = oracle.rmsnorm_rope(buf, w, ct, st, np.array([pos], np.int32), eps)
+    bt = dev(buf)
+    ops.rmsnorm_rope_heads(bt, dev(w), dev(ct), dev(st), pos0=pos, eps=eps)
+    assert_bits(host(bt), want, "rope")
+    # the reference's own check: within 1e-3 of the double-precision C reference
+    d = oracle.rmsnorm_rope_double_ref(buf, w, ct, st, [pos], eps)
+    assert np.max(np.abs(host(bt) - d)) < 1e-3
+
+
+@pytest.mark.parametrize("hd", [64, 96, 128, 160, 192, 256, 480, 512])
+def test_rmsnorm_rope_head_dims(ops, oracle, hd):
+    """Every head_dim % 32 == 0 in [64, 512] class: register rotation (hd % 64 == 0) and LDS rotation."""
+    T, H = 37, 3
+    buf = C.normal(hd, (T, H, hd))
+    w = C.norm_weight(hd + 1, hd)
+    ct, st = oracle.rope_tables(64, hd, 1e6)
+    pos = C.rng(hd + 2).integers(0, 64, T).astype(np.int32)
+    pos[0] = 0
+    want = oracle.rmsnorm_rope(buf, w, ct, st, pos, 1e-6)
+    bt = dev(buf)
+    ops.rmsnorm_rope_heads(bt, dev(w), dev(ct), dev(st), positions=dev(pos), eps=1e-6)
+    assert_bits(host(bt), want, f"rope hd={hd}")
+
+
+def test_qk_rmsnorm_rope_config2(ops, oracle):
+    """T=2048, 16 Q + 8 KV heads, hd 128, theta 1e6, positions 0..T-1, inside a fused QKV row."""
+    T, Hq, Hk, D = 2048, 16, 8, 128
+    qkv = C.normal(201, (T, (Hq + 2 * Hk) * D))
+    qw = C.norm_weight(202, D)
+    kw = C.norm_weight(203, D)
+    ct, st = oracle.rope_tables(T, D, 1e6)
+    pos = np.arange(T, dtype=np.int32)
+    q_np = qkv[:, :Hq * D].reshape(T, Hq, D)
+    k_np = qkv[:, Hq * D:(Hq + Hk) * D].reshape(T, Hk, D)
+    want_q = oracle.rmsnorm_rope(q_np, qw, ct, st, pos, 1e-6)
+    want_k = oracle.rmsnorm_rope(k_np, kw, ct, st, pos, 1e-6)
+    t = dev(qkv)
+    q = t[:, :Hq * D].view(T, Hq, D)
+    k = t[:, Hq * D:(Hq + Hk) * D].view(T, Hk, D)
+    ops.qk_rmsnorm_rope(q, k, dev(qw), dev(kw), dev(ct), dev(st), positions=dev(pos), eps=1e-6)
+    out = host(t)
+    assert_bits(out[:, :Hq * D].reshape(T, Hq, D), want_q, "q")
+    assert_bits(out[:, Hq * D:(Hq + Hk) * D].reshape(T, Hk, D), want_k, "k")
+    assert_bits(out[:, (Hq + Hk) * D:], qkv[:, (Hq + Hk) * D:], "v untouched")
+
+
+def test_rope_position_outside_tables_gives_nan(ops, oracle):
+    buf = C.normal(9, (3, 2, 64))
+    w = C.norm_weight(10, 64)
+    ct, st = oracle.rope_tables(8, 64, 1e4)
+    pos = np.array([3, 8, 0], np.int32)  # 8 is past the 8-row tables
+    bt = dev(buf)
+    ops.rmsnorm_rope_heads(bt, dev(w), dev(ct), dev(st), positions=dev(pos))
+    got = host(bt)
+    want = oracle.rmsnorm_rope(buf[[0, 2]], w, ct, st, pos[[0, 2]], 1e-6)
+    assert_bits(got[[0, 2]], want, "valid tokens")
+    assert np.isnan(got[1]).all()
+
+
+def test_rope_tables_builder(ops, oracle):
+    c, s = ops.rope_tables(4096, 128, 1e6)
+    wc, ws = oracle.rope_tables(4096, 128, 1e6)
+    assert np.max(np.abs(host(c) - wc)) <= 1e-7 and np.max(np.abs(host(s) - ws)) <= 1e-7
+
+
+# --------------------------------------------------------------------------- SwiGLU (a5, a6)
+
+SPECIAL = np.array([0.0, -0.0, 1.0, -1.0, 80.0, -80.0, 80.5, -80.5, 100.0, -100.0, 1e-30, -1e-30, 3e38, -3e38,
+                    np.inf, -np.inf, np.nan, 0.5, 88.7, -88.7, 1e-45, 2.0 ** -126], np.float32)
+
+
+def test_swiglu_special_values(ops, oracle):
+    g = np.repeat(SPECIAL, SPECIAL.size)
+    u = np.tile(SPECIAL, SPECIAL.size)
+    want = oracle.swiglu(g, u)
+    got = ops.swiglu(dev(g), dev(u))
+    assert_bits(host(got), want, "swiglu special")
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1023, 4096, 100003])
+def test_swiglu_lengths(ops, oracle, n):
+    g = C.normal(n, n, 1.5)
+    u = C.normal(n + 1, n, 1.5)
+    assert_bits(host(ops.swiglu(dev(g), dev(u))), oracle.swiglu(g, u), "swiglu")
+
+
+def test_swiglu_config3_and_in_place(ops, oracle):
+    """gate, up [4096, 6144] ~N(0, 1.5); also in place over gate as .pq_ffn_silu does."""
+    g = C.normal(301, (4096, 6144), 1.5)
+    u = C.normal(302, (4096, 6144), 1.5)
+    want = oracle.swiglu(g, u)
+    gt = dev(g)
+    ops.swiglu(gt, dev(u), out=gt)
+    got = host(gt)
+    assert_bits(got, want, "swiglu config3")
+    ref = (g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))) * u
+    rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert np.max(rel[np.abs(ref) > 1e-30]) < 1e-5
+
+
+# --------------------------------------------------------------------------- quantize (a7) and SwiGLU->Q8 (a8)
+
+@pytest.mark.parametrize("pattern", C.KT_PATTERNS)
+@pytest.mark.parametrize("n", [64, 256, 1024, 4096, 8192, 65536])
+@pytest.mark.parametrize("gs", [64, 32])
+def test_quantize_validator_patterns(ops, oracle, pattern, n, gs):
+    for seed in (12345, 67890, 11111):
+        x = C.kt_pattern(pattern, n, seed)
+        wq, ws = oracle.quantize(x[None], gs)
+        gq, gsc = ops.quantize_q8(dev(x[None]), gs=gs)
+        assert_bits(host(gq), wq, f"codes {pattern}")
+        assert_bits(host(gsc), ws, f"scales {pattern}")
+        if gs == 64:
+            kq, _ = oracle.kt_quantize_c_ref(x)
+            assert_bits(host(gq)[0], kq, "codes vs kt_quantize_c_ref")
+
+
+@pytest.mark.parametrize("rows,row_len,gs", [(1, 100, 64), (3, 1000, 64), (7, 65, 32), (2, 3, 64), (5, 130, 32),
+                                             (4, 8192, 64), (3, 257, 16)])
+def test_quantize_tails_and_ragged(ops, oracle, rows, row_len, gs):
+    x = C.normal(rows * row_len, (rows, row_len), 3.0)
+    wq, ws = oracle.quantize(x, gs)
+    gq, gsc = ops.quantize_q8(dev(x), gs=gs)
+    assert_bits(host(gq), wq, "codes")
+    assert_bits(host(gsc), ws, "scales")
+
+
+def test_quantize_non_finite(ops, oracle):
+    x = C.normal(1, (4, 64))
+    x[0, 5] = np.inf
+    x[2, 63] = np.nan
+    x[3, :] = 0.0
+    wq, ws = oracle.quantize(x, 64)
+    gq, gsc = ops.quantize_q8(dev(x), gs=64)
+    # rows without NaN: bit-exact (an Inf row gives scale Inf, codes 0 and -127 on both sides)
+    assert_bits(host(gq)[[0, 1, 3]], wq[[0, 1, 3]], "codes")
+    assert_bits(host(gsc)[[0, 1, 3]], ws[[0, 1, 3]], "scales")
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+@pytest.mark.parametrize("rows,hidden", [(1, 64), (3, 192), (16, 8192), (5, 96)])
+def test_swiglu_q8_shapes(ops, oracle, gs, rows, hidden):
+    if hidden % gs:
+        pytest.skip("hidden must be a multiple of gs on this path")
+    g = C.normal(rows + hidden, (rows, hidden), 1.5)
+    u = C.normal(rows + hidden + 1, (rows, hidden), 1.5)
+    wq, ws = oracle.swiglu_q8(g, u, gs)
+    gq, gsc = ops.swiglu_q8(dev(g), dev(u), gs=gs)
+    assert_bits(host(gq), wq, "codes")
+    assert_bits(host(gsc), ws, "scales")
+
+
+def test_swiglu_q8_config4(ops, oracle):
+    """gate, up [4096, 8192] ~N(0, 1.5), 32-element blocks."""
+    g = C.normal(401, (4096, 8192), 1.5)
+    u = C.normal(402, (4096, 8192), 1.5)
+    wq, ws = oracle.swiglu_q8(g, u, 32)
+    gq, gsc = ops.swiglu_q8(dev(g), dev(u), gs=32)
+    assert_bits(host(gq), wq, "codes")
+    assert_bits(host(gsc), ws, "scales")

@@ -1,0 +1,96 @@
+"""ctypes binding of libv7g.so (the HIP/gfx950 library; C ABI in include/v7g_lib.h).
+
+The library must have been built (``v7multiplikator_amd.build.build_library()``
+or ``__graft_entry__.build()``); there is no fallback path: a missing library
+raises at first use.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libv7g.so")
+
+V7G_OK = 0
+V7G_ERR_NULL = 1
+V7G_ERR_SHAPE = 2
+V7G_ERR_ALIGN = 3
+V7G_ERR_HIP = 4
+V7G_ERR_NO_TABLES = 5
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_ll = ctypes.c_longlong
+_f = ctypes.c_float
+
+# Plain-C (sysv) entries and their signatures.  The ms_abi drop-in entries
+# (v7s_*, v7d_quantize) are exported too but are meant for v7_lib.h-style hosts;
+# the C++ loadtest calls them.
+SIGNATURES = {
+    "v7g_init": (_i, []),
+    "v7g_set_stream": (None, [_vp]),
+    "v7g_get_stream": (_vp, []),
+    "v7g_sync": (_i, []),
+    "v7g_set_rms_eps": (None, [_f]),
+    "v7g_get_rms_eps": (_f, []),
+    "v7g_get_last_error": (_i, []),
+    "v7g_clear_last_error": (None, []),
+    "v7g_error_string": (ctypes.c_char_p, [_i]),
+    "v7g_get_rope_tables": (_i, [_vp, _vp, _vp, _vp]),
+    "v7g_rope_init": (_i, [_i, _f, _i]),
+    "v7g_build_rope_tables": (_i, [_vp, _vp, _i, _i, _f]),
+    "v7g_fused_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
+    "v7g_rmsnorm_rope_heads": (_i, [_vp, _i, _ll, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _f]),
+    "v7g_qk_rmsnorm_rope": (_i, [_vp, _ll, _i, _vp, _vp, _ll, _i, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _i, _f]),
+    "v7g_swiglu_f32": (_i, [_vp, _vp, _vp, _ll]),
+    "v7g_swiglu_q8": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+    "v7g_quantize_q8": (_i, [_vp, _vp, _vp, _i, _i, _i]),
+    "v7g_embedding_gather_q8": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i]),
+}
+
+# ms_abi drop-in entries (reference names; not callable through ctypes on Linux).
+DROP_IN = [
+    "v7s_fused_add_rmsnorm",
+    "v7s_rmsnorm_rope_heads",
+    "v7d_quantize",
+    "v7s_embedding_row",
+    "v7s_swiglu_row",
+    "v7s_swiglu_quantize_row",
+    "v7s_rope_init",
+]
+
+_lib = None
+
+
+class V7GError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        self.code = code
+        super().__init__(f"{what}: v7g error {code} ({error_string(code)})")
+
+
+def load():
+    """Returns the loaded library; raises if it was never built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: the HIP library has not been built "
+                "(run `python -c 'import __graft_entry__ as g; g.build()'`)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def error_string(code: int) -> str:
+    s = load().v7g_error_string(int(code))
+    return s.decode() if s else "?"
+
+
+def check(rc: int, what: str) -> None:
+    if rc != V7G_OK:
+        load().v7g_clear_last_error()
+        raise V7GError(rc, what)

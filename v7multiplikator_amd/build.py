@@ -1,0 +1,77 @@
+"""Builds libv7g.so for gfx950 with hipcc, in-tree (next to this file).
+
+    python -m v7multiplikator_amd.build
+
+Flags: -O3, -ffp-contract=off (every a*b+c stays two roundings; the kernels
+place every fused multiply-add explicitly, as the reference places vfmadd),
+packed-FP32 instructions disabled (-Xclang -target-feature -Xclang
+-packed-fp32-ops), default correctly rounded f32 division and sqrt.
+"""
+from __future__ import annotations
+
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "libv7g.so")
+ARCH = os.environ.get("V7G_OFFLOAD_ARCH", "gfx950")
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def sources():
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compiles every csrc/*.hip into libv7g.so; returns its path."""
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *sources()]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")
+    if verbose and out.strip():
+        print(out)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_loadtest(verbose: bool = False) -> str:
+    """Builds the C++ harness csrc/v7g_loadtest.cpp (host only, dlopens libv7g.so)."""
+    src = os.path.join(CSRC, "v7g_loadtest.cpp")
+    exe = os.path.join(PKG, "v7g_loadtest")
+    cmd = ["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-I", os.path.join(ROOT, "include"),
+           "-I", "/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", "-o", exe, src, "-ldl",
+           "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed ({res.returncode}):\n{res.stdout}{res.stderr}")
+    return exe
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))
+    if os.path.exists(os.path.join(CSRC, "v7g_loadtest.cpp")):
+        print(build_loadtest(verbose=True))
+    sys.exit(0)

@@ -1,0 +1,198 @@
+// k_rmsnorm_rope.hip -- per-head RMSNorm + rotate-half RoPE over Q/K heads, gfx950.
+//
+// Reference: v7s_rmsnorm_rope_heads(buf, n_heads, head_dim, norm_weight, cos,
+// sin, pos, rope_max_dim), src/asm/rmsnorm_rope_dispatch.inc:11-52, one job per
+// head running RMSNORM_ROPE_BODY (src/asm/v7_macros.inc:263-340):
+//   sumsq: 32-element blocks, elements 0-7 of each block into accumulator A,
+//          8-15 into B, 16-23 into C, 24-31 into D (FMA); (A+B)+(C+D); HADD_YMM.
+//   scale: 1/sqrt(sumsq/head_dim + eps).
+//   pos == 0: x = (x*scale)*w, no rotation.
+//   pos  > 0: xe = (x_j*scale)*w_j, xo = (x_{j+h}*scale)*w_{j+h},
+//             out_j = fma(-xo, sin_j, xe*cos_j), out_{j+h} = fma(xo, cos_j, xe*sin_j).
+// cos/sin rows are table + pos*rope_max_dim.
+//
+// gfx950 layout: 8 lanes per head, 8 heads per wave.  Lane m of a head holds
+// the float4 at x[4m + 32k] for every 32-element block k, so each of the 32
+// FMA chains (YMM accumulator q, lane j <-> element 8q + j of every block) is
+// lane-local and runs in the reference order; the xor exchanges 2, 4, 1 are
+// exactly the (A+B)+(C+D) and HADD_YMM pairings.  When head_dim % 64 == 0 the
+// rotate-half partner of block k is block k + K/2 in the same lane, so the
+// rotation happens in registers; otherwise the normalised head goes through
+// LDS to meet its partner.  The result is bit-identical to the reference.
+#include "v7g_device.h"
+#include "v7g_internal.h"
+
+namespace v7g {
+
+struct RopeArgs {
+  RopeSide side[2];
+  int n_sides;
+  int heads_per_token;  // side[0].n_heads + side[1].n_heads
+  unsigned n_units;     // n_tokens * heads_per_token
+  int head_dim;
+  const float *cos_table;
+  const float *sin_table;
+  const int32_t *positions;  // nullptr: pos = pos0 + token
+  int pos0;
+  int rope_max_dim;
+  int table_rows;  // positions available in cos/sin; others give NaN rows
+  float eps;
+};
+
+template <int K, bool REG_ROTATE>
+__global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RopeArgs a) {
+  constexpr int HD = 32 * K;
+  __shared__ float lds[REG_ROTATE ? 1 : 32 * HD];  // 32 heads per block when rotating through LDS
+  const int m = threadIdx.x & 7;
+  const unsigned unit = (blockIdx.x * 256u + threadIdx.x) >> 3;
+  const bool live = unit < a.n_units;
+  const unsigned uu = live ? unit : 0u;
+  const unsigned t = uu / (unsigned)a.heads_per_token;
+  const int h = (int)(uu - t * (unsigned)a.heads_per_token);
+  const int sd = (a.n_sides > 1 && h >= a.side[0].n_heads) ? 1 : 0;
+  const int hs = h - (sd ? a.side[0].n_heads : 0);
+  float *x_ptr = a.side[sd].buf + (size_t)t * (size_t)a.side[sd].token_stride + (size_t)hs * HD + 4 * m;
+  const float *w_ptr = a.side[sd].norm_weight + 4 * m;
+  int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
+  // A position outside the tables cannot be read: its heads become NaN.
+  const bool bad_pos = pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
+  if (bad_pos) pos = 0;
+
+  float4 x[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    x[k] = live ? *reinterpret_cast<const float4 *>(x_ptr + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    acc.x = __builtin_fmaf(x[k].x, x[k].x, acc.x);
+    acc.y = __builtin_fmaf(x[k].y, x[k].y, acc.y);
+    acc.z = __builtin_fmaf(x[k].z, x[k].z, acc.z);
+    acc.w = __builtin_fmaf(x[k].w, x[k].w, acc.w);
+  }
+  // A+B and C+D: lane m with m^2; (A+B)+(C+D): m with m^4; HADD_YMM first
+  // step v_i + v_{i+4}: m with m^1 (lanes 0/1 hold YMM lanes 0-3 / 4-7).
+  acc.x = acc.x + xor_f(acc.x, 2); acc.y = acc.y + xor_f(acc.y, 2);
+  acc.z = acc.z + xor_f(acc.z, 2); acc.w = acc.w + xor_f(acc.w, 2);
+  acc.x = acc.x + xor_f(acc.x, 4); acc.y = acc.y + xor_f(acc.y, 4);
+  acc.z = acc.z + xor_f(acc.z, 4); acc.w = acc.w + xor_f(acc.w, 4);
+  acc.x = acc.x + xor_f(acc.x, 1); acc.y = acc.y + xor_f(acc.y, 1);
+  acc.z = acc.z + xor_f(acc.z, 1); acc.w = acc.w + xor_f(acc.w, 1);
+  const float t0 = acc.x + acc.y;
+  const float t2 = acc.z + acc.w;
+  const float ss = t0 + t2;
+  const float s = rms_scale(ss, (float)HD, a.eps);
+
+  float4 xn[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    float4 w = *reinterpret_cast<const float4 *>(w_ptr + 32 * k);
+    xn[k] = make_float4((x[k].x * s) * w.x, (x[k].y * s) * w.y, (x[k].z * s) * w.z, (x[k].w * s) * w.w);
+  }
+
+  if (bad_pos) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) xn[k] = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+  }
+  const size_t row = (size_t)pos * (size_t)a.rope_max_dim;
+  if constexpr (REG_ROTATE) {
+    if (pos != 0) {
+      const float *cr = a.cos_table + row + 4 * m;
+      const float *sr = a.sin_table + row + 4 * m;
+      constexpr int KH = K / 2;
+#pragma unroll
+      for (int k = 0; k < KH; ++k) {
+        float4 c = *reinterpret_cast<const float4 *>(cr + 32 * k);
+        float4 sn = *reinterpret_cast<const float4 *>(sr + 32 * k);
+        float4 e = xn[k], od = xn[k + KH];
+        xn[k] = make_float4(__builtin_fmaf(-od.x, sn.x, e.x * c.x), __builtin_fmaf(-od.y, sn.y, e.y * c.y),
+                            __builtin_fmaf(-od.z, sn.z, e.z * c.z), __builtin_fmaf(-od.w, sn.w, e.w * c.w));
+        xn[k + KH] = make_float4(__builtin_fmaf(od.x, c.x, e.x * sn.x), __builtin_fmaf(od.y, c.y, e.y * sn.y),
+                                 __builtin_fmaf(od.z, c.z, e.z * sn.z), __builtin_fmaf(od.w, c.w, e.w * sn.w));
+      }
+    }
+  } else {
+    // The partner of element e is e +- HD/2, in another lane: every head of
+    // the block (32 of them, HD floats each) goes through LDS.  All threads
+    // reach the barrier; the rotation itself is skipped at pos 0.
+    float *hb = lds + (threadIdx.x >> 3) * HD;
+#pragma unroll
+    for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(hb + 4 * m + 32 * k) = xn[k];
+    __syncthreads();
+    if (pos != 0) {
+      constexpr int HALF = HD / 2;
+      const float *cr = a.cos_table + row;
+      const float *sr = a.sin_table + row;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        float cur[4] = {xn[k].x, xn[k].y, xn[k].z, xn[k].w};
+        float out[4];
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+          const int e = 4 * m + 32 * k + c4;
+          if (e < HALF) {
+            out[c4] = __builtin_fmaf(-hb[e + HALF], sr[e], cur[c4] * cr[e]);
+          } else {
+            const int j = e - HALF;
+            out[c4] = __builtin_fmaf(cur[c4], cr[j], hb[j] * sr[j]);
+          }
+        }
+        xn[k] = make_float4(out[0], out[1], out[2], out[3]);
+      }
+    }
+  }
+
+  if (live) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(x_ptr + 32 * k) = xn[k];
+  }
+}
+
+template <int K>
+static void launch_k(const RopeArgs &a, hipStream_t stream) {
+  unsigned blocks = (a.n_units + 31u) / 32u;
+  if ((32 * K) % 64 == 0)
+    hipLaunchKernelGGL((rmsnorm_rope_kernel<K, true>), dim3(blocks), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((rmsnorm_rope_kernel<K, false>), dim3(blocks), dim3(256), 0, stream, a);
+}
+
+void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int head_dim, const float *cos_table,
+                         const float *sin_table, const int32_t *positions, int pos0, int rope_max_dim, int table_rows,
+                         float eps, hipStream_t stream) {
+  RopeArgs a;
+  a.n_sides = n_sides;
+  a.side[0] = sides[0];
+  a.side[1] = n_sides > 1 ? sides[1] : sides[0];
+  a.heads_per_token = sides[0].n_heads + (n_sides > 1 ? sides[1].n_heads : 0);
+  a.n_units = (unsigned)n_tokens * (unsigned)a.heads_per_token;
+  a.head_dim = head_dim;
+  a.cos_table = cos_table;
+  a.sin_table = sin_table;
+  a.positions = positions;
+  a.pos0 = pos0;
+  a.rope_max_dim = rope_max_dim;
+  a.table_rows = table_rows;
+  a.eps = eps;
+  switch (head_dim / 32) {
+    case 2: launch_k<2>(a, stream); break;
+    case 3: launch_k<3>(a, stream); break;
+    case 4: launch_k<4>(a, stream); break;
+    case 5: launch_k<5>(a, stream); break;
+    case 6: launch_k<6>(a, stream); break;
+    case 7: launch_k<7>(a, stream); break;
+    case 8: launch_k<8>(a, stream); break;
+    case 9: launch_k<9>(a, stream); break;
+    case 10: launch_k<10>(a, stream); break;
+    case 11: launch_k<11>(a, stream); break;
+    case 12: launch_k<12>(a, stream); break;
+    case 13: launch_k<13>(a, stream); break;
+    case 14: launch_k<14>(a, stream); break;
+    case 15: launch_k<15>(a, stream); break;
+    case 16: launch_k<16>(a, stream); break;
+    default: break;
+  }
+}
+
+}  // namespace v7g

@@ -1,0 +1,347 @@
+// v7g_api.hip -- the C ABI of libv7g.so: argument validation, stream, errors,
+// RoPE tables, and the launches.  Declarations and contracts: include/v7g_lib.h.
+//
+// The reference dispatches these kernels through its CPU job pool
+// (DISPATCH_EXECUTE, src/asm/dispatch_execute.inc:5-93) or runs them on the
+// caller thread; here every call validates on the host and enqueues one HIP
+// launch on the library stream.  No entry allocates except the RoPE table
+// builders.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "v7g_internal.h"
+#include "../../include/v7g_lib.h"
+
+namespace {
+
+std::atomic<hipStream_t> g_stream{nullptr};
+std::atomic<float> g_eps{1e-6f};
+std::atomic<int> g_err{V7G_OK};
+
+std::mutex g_rope_mu;
+float *g_rope_cos = nullptr;
+float *g_rope_sin = nullptr;
+int g_rope_half = 0;
+int g_rope_npos = 0;
+
+constexpr int kRopeMaxPositions = 131072;  // ROPE_INTERNAL_MAX_SEQ_LEN, src/asm/fused_f32_kernel.inc:9
+constexpr int kMaxNormDim = 16384;         // LDS row staging limit of the add+RMSNorm kernel
+
+int fail(int code) {
+  int expected = V7G_OK;
+  g_err.compare_exchange_strong(expected, code);
+  return code;
+}
+
+int check_launch() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? V7G_OK : fail(V7G_ERR_HIP);
+}
+
+bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_add_rmsnorm(const float *o, const float *residual, const float *add, const float *weight, int rows, int dim) {
+  if (rows < 0 || dim <= 0 || dim % 8 != 0 || dim > kMaxNormDim) return V7G_ERR_SHAPE;
+  if (rows == 0) return V7G_OK;  // nothing to touch: empty tensors may carry NULL pointers
+  if (!o || !residual || !add || !weight) return V7G_ERR_NULL;
+  if (!al16(o) || !al16(residual) || !al16(add) || !al16(weight)) return V7G_ERR_ALIGN;
+  return V7G_OK;
+}
+
+int check_rope_common(int n_tokens, int head_dim, const float *cos_table, const float *sin_table, int rope_max_dim,
+                      int table_rows) {
+  if (n_tokens < 0 || head_dim < 64 || head_dim > 512 || head_dim % 32 != 0) return V7G_ERR_SHAPE;
+  if (rope_max_dim < head_dim / 2 || rope_max_dim % 4 != 0 || table_rows < 0) return V7G_ERR_SHAPE;
+  if (n_tokens == 0) return V7G_OK;
+  if (!cos_table || !sin_table) return V7G_ERR_NULL;
+  if (!al16(cos_table) || !al16(sin_table)) return V7G_ERR_ALIGN;
+  return V7G_OK;
+}
+
+int check_rope_side(const float *buf, long long token_stride, int n_heads, int head_dim, const float *w,
+                    int n_tokens) {
+  if (n_heads <= 0 || token_stride % 4 != 0) return V7G_ERR_SHAPE;
+  if (n_tokens > 1 && token_stride < (long long)n_heads * head_dim) return V7G_ERR_SHAPE;
+  if (n_tokens == 0) return V7G_OK;
+  if (!buf || !w) return V7G_ERR_NULL;
+  if (!al16(buf) || !al16(w)) return V7G_ERR_ALIGN;
+  return V7G_OK;
+}
+
+// Host RoPE table builder: src/asm/fused_f32_kernel.inc:69-147,257-303 (plain
+// rope type).  freq_j = base^(-j/half), computed in extended precision and
+// kept as a double as the reference stores it; angle = freq_j * pos in
+// extended precision; cos/sin rounded to float.
+void build_tables_host(std::vector<float> &c, std::vector<float> &s, int n_pos, int half, float base) {
+  std::vector<double> freq(half);
+  for (int j = 0; j < half; ++j)
+    freq[j] = (double)std::pow((long double)base, -(long double)j / (long double)half);
+  c.resize((size_t)n_pos * half);
+  s.resize((size_t)n_pos * half);
+  unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  std::vector<std::thread> th;
+  for (unsigned w = 0; w < nt; ++w) {
+    th.emplace_back([&, w]() {
+      for (int p = (int)w; p < n_pos; p += (int)nt)
+        for (int j = 0; j < half; ++j) {
+          long double a = (long double)freq[j] * (long double)p;
+          c[(size_t)p * half + j] = (float)std::cos(a);
+          s[(size_t)p * half + j] = (float)std::sin(a);
+        }
+    });
+  }
+  for (auto &t : th) t.join();
+}
+
+hipStream_t stream() { return g_stream.load(std::memory_order_relaxed); }
+
+}  // namespace
+
+extern "C" {
+
+// ---------------------------------------------------------------- control
+
+int v7g_init(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(V7G_ERR_HIP);
+  if (hipFree(nullptr) != hipSuccess) return fail(V7G_ERR_HIP);
+  return V7G_OK;
+}
+
+void v7g_set_stream(void *s) { g_stream.store(reinterpret_cast<hipStream_t>(s)); }
+void *v7g_get_stream(void) { return reinterpret_cast<void *>(g_stream.load()); }
+
+int v7g_sync(void) { return hipStreamSynchronize(stream()) == hipSuccess ? V7G_OK : fail(V7G_ERR_HIP); }
+
+void v7g_set_rms_eps(float eps) { g_eps.store(eps); }
+float v7g_get_rms_eps(void) { return g_eps.load(); }
+
+int v7g_get_last_error(void) { return g_err.load(); }
+void v7g_clear_last_error(void) { g_err.store(V7G_OK); }
+
+const char *v7g_error_string(int code) {
+  switch (code) {
+    case V7G_OK: return "ok";
+    case V7G_ERR_NULL: return "a required pointer is NULL";
+    case V7G_ERR_SHAPE: return "a size violates the kernel contract";
+    case V7G_ERR_ALIGN: return "a pointer is not aligned as the kernel needs";
+    case V7G_ERR_HIP: return "the HIP runtime reported an error";
+    case V7G_ERR_NO_TABLES: return "RoPE tables requested before v7s_rope_init";
+    default: return "unknown error";
+  }
+}
+
+int v7g_build_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base) {
+  if (!cos_table || !sin_table) return fail(V7G_ERR_NULL);
+  if (n_pos <= 0 || n_pos > kRopeMaxPositions || head_dim < 2 || head_dim % 2 != 0 || head_dim > 1024)
+    return fail(V7G_ERR_SHAPE);
+  std::vector<float> c, s;
+  int half = head_dim / 2;
+  build_tables_host(c, s, n_pos, half, rope_base);
+  size_t bytes = c.size() * sizeof(float);
+  if (hipMemcpy(cos_table, c.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) return fail(V7G_ERR_HIP);
+  if (hipMemcpy(sin_table, s.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) return fail(V7G_ERR_HIP);
+  return V7G_OK;
+}
+
+int v7g_rope_init(int head_dim, float rope_base, int n_pos) {
+  if (n_pos <= 0 || n_pos > kRopeMaxPositions || head_dim < 2 || head_dim % 2 != 0 || head_dim > 1024)
+    return fail(V7G_ERR_SHAPE);
+  std::lock_guard<std::mutex> lk(g_rope_mu);
+  if (g_rope_cos) {
+    // Stream-ordered release: launches already queued may still read them.
+    if (hipStreamSynchronize(stream()) != hipSuccess) return fail(V7G_ERR_HIP);
+    (void)hipFree(g_rope_cos);
+    (void)hipFree(g_rope_sin);
+    g_rope_cos = g_rope_sin = nullptr;
+    g_rope_half = g_rope_npos = 0;
+  }
+  int half = head_dim / 2;
+  size_t bytes = (size_t)n_pos * half * sizeof(float);
+  float *c = nullptr, *s = nullptr;
+  if (hipMalloc(&c, bytes) != hipSuccess) return fail(V7G_ERR_HIP);
+  if (hipMalloc(&s, bytes) != hipSuccess) {
+    (void)hipFree(c);
+    return fail(V7G_ERR_HIP);
+  }
+  int rc = v7g_build_rope_tables(c, s, n_pos, head_dim, rope_base);
+  if (rc != V7G_OK) {
+    (void)hipFree(c);
+    (void)hipFree(s);
+    return rc;
+  }
+  g_rope_cos = c;
+  g_rope_sin = s;
+  g_rope_half = half;
+  g_rope_npos = n_pos;
+  return V7G_OK;
+}
+
+int v7g_get_rope_tables(float **cos_table, float **sin_table, int *rope_max_dim, int *n_pos) {
+  std::lock_guard<std::mutex> lk(g_rope_mu);
+  if (!g_rope_cos) return fail(V7G_ERR_NO_TABLES);
+  if (cos_table) *cos_table = g_rope_cos;
+  if (sin_table) *sin_table = g_rope_sin;
+  if (rope_max_dim) *rope_max_dim = g_rope_half;
+  if (n_pos) *n_pos = g_rope_npos;
+  return V7G_OK;
+}
+
+// ---------------------------------------------------------------- batched
+
+int v7g_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
+                          float eps) {
+  int rc = check_add_rmsnorm(o, residual, add, weight, rows, dim);
+  if (rc) return fail(rc);
+  if (rows == 0) return V7G_OK;
+  v7g::launch_fused_add_rmsnorm(o, residual, add, weight, rows, dim, eps, stream());
+  return check_launch();
+}
+
+int v7g_rmsnorm_rope_heads(float *buf, int n_tokens, long long token_stride, int n_heads, int head_dim,
+                           const float *norm_weight, const float *cos_table, const float *sin_table,
+                           const int32_t *positions, int pos0, int rope_max_dim, int table_rows, float eps) {
+  int rc = check_rope_common(n_tokens, head_dim, cos_table, sin_table, rope_max_dim, table_rows);
+  if (!rc) rc = check_rope_side(buf, token_stride, n_heads, head_dim, norm_weight, n_tokens);
+  if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
+  if (rc) return fail(rc);
+  if (n_tokens == 0) return V7G_OK;
+  v7g::RopeSide side{buf, token_stride, n_heads, norm_weight};
+  v7g::launch_rmsnorm_rope(&side, 1, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
+                           table_rows, eps, stream());
+  return check_launch();
+}
+
+int v7g_qk_rmsnorm_rope(float *q, long long q_token_stride, int n_q_heads, const float *q_norm_weight, float *k,
+                        long long k_token_stride, int n_kv_heads, const float *k_norm_weight, int n_tokens,
+                        int head_dim, const float *cos_table, const float *sin_table, const int32_t *positions,
+                        int pos0, int rope_max_dim, int table_rows, float eps) {
+  int rc = check_rope_common(n_tokens, head_dim, cos_table, sin_table, rope_max_dim, table_rows);
+  if (!rc) rc = check_rope_side(q, q_token_stride, n_q_heads, head_dim, q_norm_weight, n_tokens);
+  if (!rc) rc = check_rope_side(k, k_token_stride, n_kv_heads, head_dim, k_norm_weight, n_tokens);
+  if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
+  if (rc) return fail(rc);
+  if (n_tokens == 0) return V7G_OK;
+  v7g::RopeSide sides[2] = {{q, q_token_stride, n_q_heads, q_norm_weight},
+                            {k, k_token_stride, n_kv_heads, k_norm_weight}};
+  v7g::launch_rmsnorm_rope(sides, 2, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
+                           table_rows, eps, stream());
+  return check_launch();
+}
+
+int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n) {
+  if (n < 0) return fail(V7G_ERR_SHAPE);
+  if (n == 0) return V7G_OK;
+  if (!out || !gate || !up) return fail(V7G_ERR_NULL);
+  if (!al16(out) || !al16(gate) || !al16(up)) return fail(V7G_ERR_ALIGN);
+  v7g::launch_swiglu_f32(out, gate, up, n, stream());
+  return check_launch();
+}
+
+static int check_quant(const int8_t *out_q, const float *out_s, int rows, int row_len, int gs) {
+  if (rows < 0 || row_len <= 0 || gs < 1 || gs > 4096) return V7G_ERR_SHAPE;
+  if ((long long)rows * row_len >= (1LL << 40)) return V7G_ERR_SHAPE;
+  if (rows == 0) return V7G_OK;
+  if (!out_q || !out_s) return V7G_ERR_NULL;
+  return V7G_OK;
+}
+
+int v7g_swiglu_q8(int8_t *out_q, float *out_s, const float *gate, const float *up, int rows, int hidden, int gs) {
+  int rc = check_quant(out_q, out_s, rows, hidden, gs);
+  if (!rc && rows > 0 && (!gate || !up)) rc = V7G_ERR_NULL;
+  if (rc) return fail(rc);
+  if (rows == 0) return V7G_OK;
+  v7g::launch_quantize_q8(out_q, out_s, nullptr, gate, up, rows, hidden, gs, stream());
+  return check_launch();
+}
+
+int v7g_quantize_q8(int8_t *out_q, float *out_s, const float *x, int rows, int row_len, int gs) {
+  int rc = check_quant(out_q, out_s, rows, row_len, gs);
+  if (!rc && rows > 0 && !x) rc = V7G_ERR_NULL;
+  if (rc) return fail(rc);
+  if (rows == 0) return V7G_OK;
+  v7g::launch_quantize_q8(out_q, out_s, x, nullptr, nullptr, rows, row_len, gs, stream());
+  return check_launch();
+}
+
+int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const int8_t *table_q,
+                            const float *table_s, int dim, int vocab) {
+  if (n_tokens < 0 || dim <= 0 || dim % 64 != 0 || vocab <= 0) return fail(V7G_ERR_SHAPE);
+  if (n_tokens == 0) return V7G_OK;
+  if (!out || !ids || !table_q || !table_s) return fail(V7G_ERR_NULL);
+  if ((long long)n_tokens * (dim / 16) >= (1LL << 32)) return fail(V7G_ERR_SHAPE);
+  if (!al16(out) || !al16(table_q) || ((uintptr_t)table_s & 3u) || ((uintptr_t)ids & 3u))
+    return fail(V7G_ERR_ALIGN);
+  if (n_tokens == 0) return V7G_OK;
+  v7g::launch_embedding_gather(out, ids, n_tokens, table_q, table_s, dim, vocab, stream());
+  return check_launch();
+}
+
+// ---------------------------------------------------------------- drop-in (ms_abi)
+
+V7_ABI void v7s_fused_add_rmsnorm(float *o, float *residual, float *add, float *weight, int dim) {
+  v7g_fused_add_rmsnorm(o, residual, add, weight, 1, dim, g_eps.load());
+}
+
+V7_ABI void v7s_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, float *norm_weight, float *cos_table,
+                                   float *sin_table, int pos, int rope_max_dim) {
+  if (pos < 0) {
+    fail(V7G_ERR_SHAPE);
+    return;
+  }
+  // The caller's tables hold at least pos+1 rows (the reference offsets them by
+  // pos*rope_max_dim without a bound).
+  v7g_rmsnorm_rope_heads(buf, 1, (long long)n_heads * head_dim, n_heads, head_dim, norm_weight, cos_table, sin_table,
+                         nullptr, pos, rope_max_dim, pos + 1, g_eps.load());
+}
+
+V7_ABI void v7d_quantize(char *out_q, float *in_x, float *out_s, int n) {
+  if (n <= 0) {
+    if (n < 0) fail(V7G_ERR_SHAPE);
+    return;
+  }
+  v7g_quantize_q8(reinterpret_cast<int8_t *>(out_q), out_s, in_x, 1, n, 64);
+}
+
+V7_ABI void v7s_embedding_row(float *out, int token, int dim, v7g_q8_tensor *q_desc) {
+  if (!q_desc || !out) {
+    fail(V7G_ERR_NULL);
+    return;
+  }
+  if (token < 0 || dim <= 0 || dim % 64 != 0) {
+    fail(V7G_ERR_SHAPE);
+    return;
+  }
+  // One row: offset the table to the token's row and gather id 0 of a
+  // one-row table, so the kernel needs no device-side id.
+  size_t base = (size_t)token * (size_t)dim;
+  const int8_t *q = reinterpret_cast<const int8_t *>(q_desc->q) + base;
+  const float *s = q_desc->s + (base >> 6);
+  if (!al16(out) || !al16(q) || ((uintptr_t)s & 3u)) {
+    fail(V7G_ERR_ALIGN);
+    return;
+  }
+  v7g::launch_embedding_gather(out, nullptr, 1, q, s, dim, 1, stream());
+  check_launch();
+}
+
+V7_ABI void v7s_swiglu_row(float *gate_inout, float *up, int hidden) {
+  if (hidden < 0) {
+    fail(V7G_ERR_SHAPE);
+    return;
+  }
+  v7g_swiglu_f32(gate_inout, gate_inout, up, hidden);
+}
+
+V7_ABI void v7s_swiglu_quantize_row(char *out_q, float *gate, float *up, float *out_s, int hidden) {
+  v7g_swiglu_q8(reinterpret_cast<int8_t *>(out_q), out_s, gate, up, 1, hidden, 64);
+}
+
+V7_ABI void v7s_rope_init(int head_dim, float rope_base) { v7g_rope_init(head_dim, rope_base, kRopeMaxPositions); }
+
+}  // extern "C"

@@ -1,0 +1,34 @@
+// v7g_internal.h -- launchers shared between the kernel files and the C-ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace v7g {
+
+// Launchers: shapes and pointers are validated by the caller (v7g_api.hip);
+// each launcher only computes the grid and enqueues on `stream`.
+void launch_embedding_gather(float *out, const int32_t *ids, int n_tokens, const int8_t *table_q,
+                             const float *table_s, int dim, int vocab, hipStream_t stream);
+
+void launch_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
+                              float eps, hipStream_t stream);
+
+struct RopeSide {
+  float *buf;               // first head of token 0
+  long long token_stride;   // floats between consecutive tokens
+  int n_heads;
+  const float *norm_weight; // [head_dim]
+};
+void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int head_dim, const float *cos_table,
+                         const float *sin_table, const int32_t *positions, int pos0, int rope_max_dim, int table_rows,
+                         float eps, hipStream_t stream);
+
+void launch_swiglu_f32(float *out, const float *gate, const float *up, long long n, hipStream_t stream);
+
+// Q8 block quantization of `rows` rows of `row_len` floats, groups of `gs`
+// never crossing a row; with gate/up given, the quantized value is the SwiGLU
+// of the pair instead of x.
+void launch_quantize_q8(int8_t *out_q, float *out_s, const float *x, const float *gate, const float *up, int rows,
+                        int row_len, int gs, hipStream_t stream);
+
+}  // namespace v7g

@@ -1,0 +1,209 @@
+"""Torch-facing host API of the fused per-layer kernels.
+
+Mirrors the reference's kernel entry points (src/v7_lib.h:113-128,269-281) for
+batched device tensors.  Every function validates its tensors, binds the
+library to torch's current stream and makes ONE launch through the C ABI of
+libv7g.so; nothing runs on the CPU and there is no fallback: without the built
+library the first call raises.
+
+  fused_add_rmsnorm  <- v7s_fused_add_rmsnorm   (src/asm/add_rmsnorm_kernel.inc:15-129)
+  rmsnorm_rope_heads <- v7s_rmsnorm_rope_heads  (src/asm/rmsnorm_rope_dispatch.inc:11-52)
+  qk_rmsnorm_rope    <- v7s_qk_fork_heads, both sides in one launch (src/asm/qk_fork_kernel.inc:40-62)
+  swiglu             <- .pq_ffn_silu            (src/asm/prefill_q8.inc:1159-1166)
+  quantize_q8        <- v7d_quantize            (src/asm/utility_dispatch.inc:108-212)
+  swiglu_q8          <- SwiGLU then v7d_quantize (src/asm/prefill_q8.inc:1154-1183)
+  embedding_gather_q8 <- v7s_embedding_row      (src/asm/forward.inc:13-42)
+  rope_tables        <- v7s_rope_init           (src/asm/fused_dispatch.inc:58-76)
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+Q8_EMBED_GS = 64  # scale group of the Q8 embedding table (src/asm/forward.inc:14, GS=64)
+
+
+def _bind(t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise ValueError("v7g kernels take device tensors (cuda:N)")
+    _lib.load().v7g_set_stream(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need(t: torch.Tensor, dtype, name: str, contiguous: bool = True) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be on a cuda device")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def fused_add_rmsnorm(residual: torch.Tensor, add: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """residual += add (in place); returns out = rmsnorm(residual) * weight.  [rows, dim] f32."""
+    for t, n in ((residual, "residual"), (add, "add"), (weight, "weight")):
+        _need(t, torch.float32, n)
+    dim = residual.shape[-1]
+    rows = residual.numel() // dim if dim else 0
+    if add.shape != residual.shape or weight.numel() != dim:
+        raise ValueError("shape mismatch: add must match residual, weight must be [dim]")
+    if out is None:
+        out = torch.empty_like(residual)
+    _need(out, torch.float32, "out")
+    _bind(residual)
+    rc = _lib.load().v7g_fused_add_rmsnorm(out.data_ptr(), residual.data_ptr(), add.data_ptr(), weight.data_ptr(),
+                                           rows, dim, float(eps))
+    _lib.check(rc, "fused_add_rmsnorm")
+    return out
+
+
+def _heads_view(buf: torch.Tensor, name: str):
+    """[T, H, D] view with unit stride inside a token's heads; returns (T, H, D, token_stride)."""
+    if buf.dim() != 3:
+        raise ValueError(f"{name} must be [tokens, heads, head_dim]")
+    T, H, D = buf.shape
+    if buf.stride(2) != 1 or buf.stride(1) != D:
+        raise ValueError(f"{name}: heads of one token must be contiguous")
+    return T, H, D, buf.stride(0)
+
+
+def _positions(positions, T, device):
+    if positions is None:
+        return 0
+    _need(positions, torch.int32, "positions")
+    if positions.numel() != T:
+        raise ValueError("positions must hold one int32 per token")
+    return positions.data_ptr()
+
+
+def rmsnorm_rope_heads(buf: torch.Tensor, norm_weight: torch.Tensor, cos_table: torch.Tensor,
+                       sin_table: torch.Tensor, positions: torch.Tensor | None = None, pos0: int = 0,
+                       eps: float = 1e-6) -> torch.Tensor:
+    """In-place per-head RMSNorm + RoPE of buf [T, H, D] (token stride free); tables [P, rope_max_dim]."""
+    _need(buf, torch.float32, "buf", contiguous=False)
+    for t, n in ((norm_weight, "norm_weight"), (cos_table, "cos_table"), (sin_table, "sin_table")):
+        _need(t, torch.float32, n)
+    T, H, D, ts = _heads_view(buf, "buf")
+    _bind(buf)
+    rc = _lib.load().v7g_rmsnorm_rope_heads(buf.data_ptr(), T, ts, H, D, norm_weight.data_ptr(),
+                                            cos_table.data_ptr(), sin_table.data_ptr(),
+                                            _positions(positions, T, buf.device), int(pos0), cos_table.shape[-1],
+                                            cos_table.shape[0], float(eps))
+    _lib.check(rc, "rmsnorm_rope_heads")
+    return buf
+
+
+def qk_rmsnorm_rope(q: torch.Tensor, k: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
+                    cos_table: torch.Tensor, sin_table: torch.Tensor, positions: torch.Tensor | None = None,
+                    pos0: int = 0, eps: float = 1e-6) -> None:
+    """In-place RMSNorm+RoPE of Q [T, Hq, D] and K [T, Hk, D] in one launch."""
+    for t, n in ((q, "q"), (k, "k")):
+        _need(t, torch.float32, n, contiguous=False)
+    for t, n in ((q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight"), (cos_table, "cos_table"),
+                 (sin_table, "sin_table")):
+        _need(t, torch.float32, n)
+    T, Hq, D, qs = _heads_view(q, "q")
+    Tk, Hk, Dk, ks = _heads_view(k, "k")
+    if Tk != T or Dk != D:
+        raise ValueError("q and k must have the same tokens and head_dim")
+    _bind(q)
+    rc = _lib.load().v7g_qk_rmsnorm_rope(q.data_ptr(), qs, Hq, q_norm_weight.data_ptr(), k.data_ptr(), ks, Hk,
+                                         k_norm_weight.data_ptr(), T, D, cos_table.data_ptr(), sin_table.data_ptr(),
+                                         _positions(positions, T, q.device), int(pos0), cos_table.shape[-1],
+                                         cos_table.shape[0], float(eps))
+    _lib.check(rc, "qk_rmsnorm_rope")
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = (sigmoid(gate)*gate)*up, f32 elementwise; out may be gate (in place)."""
+    _need(gate, torch.float32, "gate")
+    _need(up, torch.float32, "up")
+    if up.shape != gate.shape:
+        raise ValueError("gate and up must have the same shape")
+    if out is None:
+        out = torch.empty_like(gate)
+    _need(out, torch.float32, "out")
+    _bind(gate)
+    rc = _lib.load().v7g_swiglu_f32(out.data_ptr(), gate.data_ptr(), up.data_ptr(), gate.numel())
+    _lib.check(rc, "swiglu")
+    return out
+
+
+def _q8_out(shape, row_len, gs, device, out_q, out_s):
+    rows = 1
+    for d in shape[:-1]:
+        rows *= d
+    spr = -(-row_len // gs)
+    if out_q is None:
+        out_q = torch.empty(shape, dtype=torch.int8, device=device)
+    if out_s is None:
+        out_s = torch.empty((rows, spr), dtype=torch.float32, device=device)
+    _need(out_q, torch.int8, "out_q")
+    _need(out_s, torch.float32, "out_s")
+    if out_q.numel() != rows * row_len or out_s.numel() != rows * spr:
+        raise ValueError("output buffers have the wrong size")
+    return rows, out_q, out_s
+
+
+def swiglu_q8(gate: torch.Tensor, up: torch.Tensor, gs: int = 32, out_q: torch.Tensor | None = None,
+              out_s: torch.Tensor | None = None):
+    """SwiGLU then Q8 block quantization per row: returns (codes int8 like gate, scales [rows, hidden/gs])."""
+    _need(gate, torch.float32, "gate")
+    _need(up, torch.float32, "up")
+    if up.shape != gate.shape:
+        raise ValueError("gate and up must have the same shape")
+    hidden = gate.shape[-1]
+    rows, out_q, out_s = _q8_out(gate.shape, hidden, gs, gate.device, out_q, out_s)
+    _bind(gate)
+    rc = _lib.load().v7g_swiglu_q8(out_q.data_ptr(), out_s.data_ptr(), gate.data_ptr(), up.data_ptr(), rows, hidden,
+                                   int(gs))
+    _lib.check(rc, "swiglu_q8")
+    return out_q, out_s
+
+
+def quantize_q8(x: torch.Tensor, gs: int = 64, out_q: torch.Tensor | None = None,
+                out_s: torch.Tensor | None = None):
+    """v7d_quantize per row of x [..., row_len]: returns (codes, scales [rows, ceil(row_len/gs)])."""
+    _need(x, torch.float32, "x")
+    row_len = x.shape[-1]
+    rows, out_q, out_s = _q8_out(x.shape, row_len, gs, x.device, out_q, out_s)
+    _bind(x)
+    rc = _lib.load().v7g_quantize_q8(out_q.data_ptr(), out_s.data_ptr(), x.data_ptr(), rows, row_len, int(gs))
+    _lib.check(rc, "quantize_q8")
+    return out_q, out_s
+
+
+def embedding_gather_q8(ids: torch.Tensor, table_q: torch.Tensor, table_s: torch.Tensor,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[t] = dequant(table row ids[t]); table_q [vocab, dim] int8, table_s [vocab*dim/64] f32."""
+    _need(ids, torch.int32, "ids")
+    _need(table_q, torch.int8, "table_q")
+    _need(table_s, torch.float32, "table_s")
+    if table_q.dim() != 2:
+        raise ValueError("table_q must be [vocab, dim]")
+    vocab, dim = table_q.shape
+    if table_s.numel() != vocab * dim // Q8_EMBED_GS:
+        raise ValueError("table_s must hold vocab*dim/64 scales")
+    n = ids.numel()
+    if out is None:
+        out = torch.empty((n, dim), dtype=torch.float32, device=ids.device)
+    _need(out, torch.float32, "out")
+    _bind(ids)
+    rc = _lib.load().v7g_embedding_gather_q8(out.data_ptr(), ids.data_ptr(), n, table_q.data_ptr(),
+                                             table_s.data_ptr(), dim, vocab)
+    _lib.check(rc, "embedding_gather_q8")
+    return out
+
+
+def rope_tables(n_pos: int, head_dim: int, rope_base: float, device="cuda"):
+    """Device cos/sin tables [n_pos, head_dim/2] (freq_j = base^(-j/half)), built on the host."""
+    half = head_dim // 2
+    c = torch.empty((n_pos, half), dtype=torch.float32, device=device)
+    s = torch.empty((n_pos, half), dtype=torch.float32, device=device)
+    torch.cuda.synchronize(c.device)
+    rc = _lib.load().v7g_build_rope_tables(c.data_ptr(), s.data_ptr(), n_pos, head_dim, float(rope_base))
+    _lib.check(rc, "rope_tables")
+    return c, s
