@@ -1,0 +1,176 @@
+"""The C ABI of libv7g.so without a GPU: exports, argument validation, error reporting (CPU only).
+
+Every entry point declared in include/v7g_lib.h must be exported; the batched
+entries must reject contract violations with the documented code before any
+HIP call, and the drop-in (reference-signature) entries must record them in
+the sticky error instead of aborting the host (the reference's FATAL path,
+src/asm/v7_core.inc:291-299, has no place in a GPU library).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from v7multiplikator_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "v7g_lib.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = set()
+    for m in re.finditer(r"^\s*(?:V7_ABI\s+)?(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**\s*([a-z][a-z0-9_]*)\s*\(",
+                         text, flags=re.M):
+        names.add(m.group(1))
+    return sorted(n for n in names if n.startswith(("v7g_", "v7s_", "v7d_")))
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.load()
+
+
+def test_header_declares_the_drop_in_and_batched_entries():
+    names = declared_functions()
+    for n in ("v7s_fused_add_rmsnorm", "v7s_rmsnorm_rope_heads", "v7d_quantize", "v7s_embedding_row",
+              "v7s_swiglu_row", "v7s_swiglu_quantize_row", "v7s_rope_init", "v7g_fused_add_rmsnorm",
+              "v7g_rmsnorm_rope_heads", "v7g_qk_rmsnorm_rope", "v7g_swiglu_f32", "v7g_swiglu_q8",
+              "v7g_quantize_q8", "v7g_embedding_gather_q8"):
+        assert n in names, n
+
+
+def test_library_exports_every_declared_symbol(L):
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, missing
+    for n in declared_functions():
+        assert getattr(L, n) is not None
+
+
+def test_python_binding_covers_the_plain_c_entries():
+    plain = [n for n in declared_functions() if n.startswith("v7g_")]
+    assert sorted(plain) == sorted(_lib.SIGNATURES)
+    drop_in = [n for n in declared_functions() if not n.startswith("v7g_")]
+    assert sorted(drop_in) == sorted(_lib.DROP_IN)
+
+
+def test_error_strings(L):
+    for code in range(0, 6):
+        assert _lib.error_string(code) not in ("", "unknown error")
+    assert _lib.error_string(99) == "unknown error"
+
+
+def test_eps_global_roundtrip(L):
+    old = L.v7g_get_rms_eps()
+    try:
+        L.v7g_set_rms_eps(1e-5)
+        assert abs(L.v7g_get_rms_eps() - 1e-5) < 1e-12
+    finally:
+        L.v7g_set_rms_eps(old)
+
+
+def _sticky(L, fn, *args):
+    L.v7g_clear_last_error()
+    rc = fn(*args)
+    return rc, L.v7g_get_last_error()
+
+
+FAKE = 0x10000  # a 16-byte aligned non-null address; never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("rows,dim,want", [(1, 7, 2), (1, 0, 2), (-1, 64, 2), (1, 16392, 2)])
+def test_fused_add_rmsnorm_rejects_shapes(L, rows, dim, want):
+    rc, err = _sticky(L, L.v7g_fused_add_rmsnorm, FAKE, FAKE, FAKE, FAKE, rows, dim, 1e-6)
+    assert rc == want and err == want
+
+
+def test_fused_add_rmsnorm_rejects_null_and_misaligned(L):
+    assert _sticky(L, L.v7g_fused_add_rmsnorm, None, FAKE, FAKE, FAKE, 2, 64, 1e-6) == (1, 1)
+    assert _sticky(L, L.v7g_fused_add_rmsnorm, FAKE + 4, FAKE, FAKE, FAKE, 2, 64, 1e-6) == (3, 3)
+    # rows == 0 touches nothing: OK even with NULL pointers
+    assert _sticky(L, L.v7g_fused_add_rmsnorm, None, None, None, None, 0, 64, 1e-6) == (0, 0)
+
+
+@pytest.mark.parametrize("hd", [32, 48, 544, 100])
+def test_rope_rejects_head_dims(L, hd):
+    rc, err = _sticky(L, L.v7g_rmsnorm_rope_heads, FAKE, 4, 8 * hd, 8, hd, FAKE, FAKE, FAKE, None, 0, hd // 2,
+                      16, 1e-6)
+    assert rc == 2 and err == 2
+
+
+def test_rope_rejects_short_table_rows_and_stride(L):
+    # rope_max_dim < head_dim/2
+    assert _sticky(L, L.v7g_rmsnorm_rope_heads, FAKE, 4, 1024, 8, 128, FAKE, FAKE, FAKE, None, 0, 32, 16,
+                   1e-6)[0] == 2
+    # token stride shorter than the heads of one token
+    assert _sticky(L, L.v7g_rmsnorm_rope_heads, FAKE, 4, 512, 8, 128, FAKE, FAKE, FAKE, None, 0, 64, 16,
+                   1e-6)[0] == 2
+    # misaligned positions
+    assert _sticky(L, L.v7g_rmsnorm_rope_heads, FAKE, 4, 1024, 8, 128, FAKE, FAKE, FAKE, FAKE + 2, 0, 64, 16,
+                   1e-6)[0] == 3
+    # qk form: k side checked too
+    assert _sticky(L, L.v7g_qk_rmsnorm_rope, FAKE, 4096, 32, FAKE, None, 1024, 8, FAKE, 4, 128, FAKE, FAKE, None,
+                   0, 64, 16, 1e-6)[0] == 1
+
+
+def test_quantize_and_swiglu_reject(L):
+    assert _sticky(L, L.v7g_quantize_q8, FAKE, FAKE, FAKE, 1, 64, 0)[0] == 2
+    assert _sticky(L, L.v7g_quantize_q8, FAKE, FAKE, FAKE, 1, 64, 8192)[0] == 2
+    assert _sticky(L, L.v7g_quantize_q8, None, FAKE, FAKE, 1, 64, 64)[0] == 1
+    assert _sticky(L, L.v7g_swiglu_q8, FAKE, FAKE, None, FAKE, 1, 64, 32)[0] == 1
+    assert _sticky(L, L.v7g_swiglu_f32, FAKE, FAKE, FAKE, -1)[0] == 2
+    assert _sticky(L, L.v7g_swiglu_f32, FAKE, FAKE + 8, FAKE, 16)[0] == 3
+    assert _sticky(L, L.v7g_swiglu_f32, None, None, None, 0) == (0, 0)
+
+
+def test_embedding_rejects(L):
+    assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE, FAKE, 100, 1000)[0] == 2  # dim % 64
+    assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE, FAKE, 128, 0)[0] == 2
+    assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, None, 4, FAKE, FAKE, 128, 10)[0] == 1
+    assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE + 4, FAKE, 128, 10)[0] == 3
+
+
+def test_sticky_error_keeps_the_first_code(L):
+    L.v7g_clear_last_error()
+    L.v7g_swiglu_f32(FAKE, FAKE, FAKE, -1)
+    L.v7g_quantize_q8(None, FAKE, FAKE, 1, 64, 64)
+    assert L.v7g_get_last_error() == 2
+    L.v7g_clear_last_error()
+    assert L.v7g_get_last_error() == 0
+
+
+def test_rope_table_entry_validation(L):
+    assert _sticky(L, L.v7g_rope_init, 127, ctypes.c_float(1e6), 16)[0] == 2
+    assert _sticky(L, L.v7g_rope_init, 128, ctypes.c_float(1e6), 131073)[0] == 2
+    assert _sticky(L, L.v7g_build_rope_tables, None, FAKE, 16, 128, ctypes.c_float(1e6))[0] == 1
+    assert _sticky(L, L.v7g_get_rope_tables, None, None, None, None)[0] == 5
+
+
+def test_check_raises_and_clears(L):
+    L.v7g_clear_last_error()
+    rc = L.v7g_swiglu_f32(FAKE, FAKE, FAKE, -1)
+    with pytest.raises(_lib.V7GError) as e:
+        _lib.check(rc, "swiglu")
+    assert e.value.code == 2
+    assert L.v7g_get_last_error() == 0
+
+
+def test_ops_refuse_host_tensors():
+    torch = pytest.importorskip("torch")
+    from v7multiplikator_amd import ops
+
+    x = torch.zeros(4, 64)
+    with pytest.raises(ValueError):
+        ops.swiglu(x, x)
+    with pytest.raises(ValueError):
+        ops.fused_add_rmsnorm(x, x, torch.ones(64))
+    with pytest.raises(TypeError):
+        ops.quantize_q8(x.double())

@@ -1,0 +1,371 @@
+"""Pins of the CPU oracle (oracle/v7_oracle.c, oracle/oracle.py) -- CPU only.
+
+The oracle restates the reference NASM kernels operation by operation.  These
+tests pin it with facts that do not come from the oracle itself:
+
+  * hand-derived known answers that only the reference's accumulation order
+    produces (sum of squares: four 8-lane accumulators, leftover blocks first
+    into A, (A+B)+(C+D), HADD_YMM; src/asm/add_rmsnorm_kernel.inc:29-73,
+    src/asm/v7_macros.inc:38-45,263-291);
+  * the reference validators' own checks: kt_quantize_c_ref exact codes on
+    the seven KTPAT patterns (tools/kt_utils.h:139-191,378-407,681-731), the
+    double-precision RMSNorm+RoPE reference and float add+RMSNorm reference
+    within 1e-3 (tools/kt_utils.h:450-503,820,935-1074);
+  * closed forms and invariants: exact int8 x f32 dequant, the quantizer's
+    all-zero-group scale 2^-126, absmax -> +-127, rotations by 0 and 90
+    degrees, pos = 0 without rotation, pair norms, sigmoid/SwiGLU against
+    double precision;
+  * the AVX2 restatement (the CPU baseline) against the scalar oracle, bit for bit.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from tests import common as C
+
+F = np.float32
+TWO24 = float(2 ** 24)
+
+
+def bits_equal(a, b):
+    a = np.asarray(a)
+    b = np.asarray(b)
+    if a.shape != b.shape:
+        return False
+    if a.dtype.kind == "f":
+        return bool(np.array_equal(a.view(np.uint32 if a.dtype == np.float32 else np.uint64),
+                                   b.view(np.uint32 if b.dtype == np.float32 else np.uint64)))
+    return bool(np.array_equal(a, b))
+
+
+# --------------------------------------------------------------------------- sum of squares order (a1, a2, a3)
+
+def test_sumsq_hadd_tree_known_answer(oracle):
+    """dim 32: x[0] = 4096 (square 2^24), x[1..7] = 1, rest 0.  Only accumulator A is non-zero, so the
+    HADD_YMM input is v = [2^24, 1, 1, 1, 1, 1, 1, 1]:
+      s0 = v0 + v4 = 2^24 + 1 -> 2^24 (tie to even), s1 = s2 = s3 = 2,
+      (s0 + s1) + (s2 + s3) = (2^24 + 2) + 4 = 2^24 + 6.
+    A left-to-right sum gives 2^24 (every +1 is absorbed)."""
+    x = np.zeros(32, F)
+    x[0] = 4096.0
+    x[1:8] = 1.0
+    assert float(oracle.sumsq_lanes(x)) == TWO24 + 6
+
+
+def test_sumsq_accumulator_interleave_known_answer(oracle):
+    """dim 64 (8 blocks, 2 groups): blocks 0,4 -> A, 1,5 -> B, 2 -> C, 3 -> D, lane 0 only.
+    x[0] = 4096 (A), x[32] = 1 (A: fma(1,1,2^24) = 2^24), x[8] = x[40] = 1 (B = 2), x[16] = 1 (C), x[24] = 1 (D):
+      v0 = (A + B) + (C + D) = (2^24 + 2) + 2 = 2^24 + 4.
+    One accumulator per lane in element order gives 2^24."""
+    x = np.zeros(64, F)
+    x[0] = 4096.0
+    for i in (8, 16, 24, 32, 40):
+        x[i] = 1.0
+    assert float(oracle.sumsq_lanes(x)) == TWO24 + 4
+
+
+def test_sumsq_leftover_blocks_first_known_answer(oracle):
+    """dim 40 (5 blocks, 1 leftover): the leftover block 0 goes first into A, then blocks 1..4 feed A, B, C, D.
+    x[0] = 4096 (block 0 -> A), x[24] = 1 (block 3 -> C), x[32] = 1 (block 4 -> D):
+      v0 = (2^24 + 0) + (1 + 1) = 2^24 + 2.
+    Were the leftover block taken last (blocks 0..3 -> A..D, block 4 -> A), block 4 would be absorbed into A
+    and block 3 would land in D: (2^24 + 0) + (0 + 1) = 2^24 (tie to even)."""
+    x = np.zeros(40, F)
+    x[0] = 4096.0
+    x[24] = 1.0
+    x[32] = 1.0
+    assert float(oracle.sumsq_lanes(x)) == TWO24 + 2
+
+
+def test_rms_scale_closed_form(oracle):
+    """COMPUTE_RMS_SCALE = 1/sqrt(sumsq/n + eps) in four correctly rounded steps: exact for powers of two."""
+    assert float(oracle.rms_scale(F(4 * 64), 64, 0.0)) == 0.5
+    assert float(oracle.rms_scale(F(64), 64, 0.0)) == 1.0
+    # each step rounded to binary32 (numpy float32 ops are IEEE binary32)
+    ss, n, eps = F(123.456), 128, F(1e-6)
+    want = F(1.0) / np.sqrt(F(ss / F(n)) + eps)
+    assert bits_equal(np.array([oracle.rms_scale(ss, n, float(eps))], F), np.array([want], F))
+
+
+def test_fused_add_rmsnorm_constant_row_closed_form(oracle):
+    """x = residual + add = 2 everywhere, w = 1, eps = 0: sumsq = 4*dim exactly, scale = 1/2, o = 1 exactly."""
+    for dim in (8, 24, 64, 4096):
+        r = np.full((1, dim), 1.5, F)
+        a = np.full((1, dim), 0.5, F)
+        o, rr = oracle.fused_add_rmsnorm(r, a, np.ones(dim, F), 0.0)
+        assert np.all(rr == 2.0) and np.all(o == 1.0)
+
+
+@pytest.mark.parametrize("dim", [8, 16, 24, 48, 64, 128, 256, 1024, 2048, 3072, 4096, 8192])
+@pytest.mark.parametrize("seed", [12345, 67890])
+def test_fused_add_rmsnorm_vs_validator_refs(oracle, dim, seed):
+    """tools/v_rmsnorm_validate.cpp:87-101 shapes: within 1e-3 of the float C reference (the reference's own
+    tolerance, tools/kt_utils.h:820) and within 1e-5 relative of a double-precision evaluation."""
+    r = C.validator_row(seed, dim)
+    a = C.validator_row(seed + 1, dim)
+    w = C.validator_weight(seed + 2, dim)
+    o, rr = oracle.fused_add_rmsnorm(r[None], a[None], w, 1e-6)
+    assert bits_equal(rr[0], (r + a).astype(F))  # residual update: one binary32 add per element
+    ko, _ = oracle.kt_fused_add_rmsnorm_c_ref(r, a, w, 1e-6)
+    assert np.max(np.abs(o[0] - ko)) < 1e-3
+    x = (r + a).astype(np.float64)
+    d = x / np.sqrt(np.mean(x * x) + 1e-6) * w.astype(np.float64)
+    assert np.max(np.abs(o[0] - d) / np.maximum(np.abs(d), 1e-3)) < 1e-5
+
+
+def test_fused_add_rmsnorm_benchmark_distribution(oracle):
+    """[64, 2048] ~N(0,1), w = 1+N(0,0.1): max relative error vs double below 1e-5 (the f32 bar)."""
+    r = C.normal(101, (64, 2048))
+    a = C.normal(102, (64, 2048))
+    w = C.norm_weight(103, 2048)
+    o, _ = oracle.fused_add_rmsnorm(r, a, w, 1e-6)
+    x = r.astype(np.float64) + a.astype(np.float64)
+    x = x.astype(F).astype(np.float64)
+    d = x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + 1e-6) * w
+    rel = np.abs(o - d) / np.abs(d)
+    assert np.max(rel[np.abs(d) > 1e-6]) < 1e-5
+
+
+# --------------------------------------------------------------------------- RMSNorm + RoPE (a3, a4)
+
+def _normed(oracle, x, w, eps):
+    """pos-0 output: (x*scale)*w with the lane-ordered scale; used to state the rotation invariants."""
+    return oracle.rmsnorm_rope(x, w, np.ones((1, x.shape[-1] // 2), F), np.zeros((1, x.shape[-1] // 2), F),
+                               np.zeros(x.shape[0], np.int32), eps)
+
+
+def test_rope_pos0_is_rmsnorm_only(oracle):
+    x = C.normal(1, (3, 4, 128))
+    w = C.norm_weight(2, 128)
+    ct, st = oracle.rope_tables(4, 128, 1e6)
+    got = oracle.rmsnorm_rope(x, w, ct, st, np.zeros(3, np.int32), 1e-6)
+    s = np.array([[oracle.rms_scale(oracle.sumsq_lanes(x[t, h]), 128, 1e-6) for h in range(4)] for t in range(3)], F)
+    want = ((x * s[..., None]).astype(F) * w).astype(F)
+    assert bits_equal(got, want)
+
+
+def test_rope_quarter_turn_and_identity_tables(oracle):
+    """cos = 0, sin = 1 at pos 1: out_j = -xo, out_{j+h} = xe exactly (fma(-xo, 1, xe*0), fma(xo, 0, xe*1)).
+    cos = 1, sin = 0 at pos 1: the head equals the pos-0 result exactly.  A swapped table, a wrong sign or
+    a wrong partner index fails one of these."""
+    T, H, D = 2, 3, 128
+    x = C.normal(3, (T, H, D))
+    w = C.norm_weight(4, D)
+    n = _normed(oracle, x, w, 1e-6)
+    half = D // 2
+    c90 = np.zeros((2, half), F)
+    s90 = np.zeros((2, half), F)
+    c90[1] = 0.0
+    s90[1] = 1.0
+    got = oracle.rmsnorm_rope(x, w, c90, s90, np.ones(T, np.int32), 1e-6)
+    assert bits_equal(got[..., :half], -n[..., half:])
+    assert bits_equal(got[..., half:], n[..., :half])
+    c0 = np.ones((2, half), F)
+    s0 = np.zeros((2, half), F)
+    got = oracle.rmsnorm_rope(x, w, c0, s0, np.ones(T, np.int32), 1e-6)
+    assert bits_equal(got, n)
+
+
+def test_rope_rotation_preserves_pair_norms(oracle):
+    T, H, D = 64, 4, 128
+    x = C.normal(5, (T, H, D))
+    w = C.norm_weight(6, D)
+    ct, st = oracle.rope_tables(T, D, 1e6)
+    pos = np.arange(T, dtype=np.int32)
+    got = oracle.rmsnorm_rope(x, w, ct, st, pos, 1e-6).astype(np.float64)
+    n = _normed(oracle, x, w, 1e-6).astype(np.float64)
+    h = D // 2
+    r_got = np.hypot(got[..., :h], got[..., h:])
+    r_n = np.hypot(n[..., :h], n[..., h:])
+    assert np.max(np.abs(r_got - r_n) / np.maximum(r_n, 1e-6)) < 1e-6
+
+
+@pytest.mark.parametrize("heads,hd,pos,eps", [(1, 64, 0, 1e-6), (1, 64, 7, 1e-6), (4, 64, 31, 1e-6),
+                                              (8, 128, 0, 1e-6), (16, 64, 31, 1e-6), (32, 128, 0, 1e-6),
+                                              (40, 64, 31, 1e-6), (40, 128, 7, 1e-6), (32, 64, 31, 1e-5),
+                                              (8, 64, 7, 1e-5)])
+@pytest.mark.parametrize("seed", [12345, 67890])
+def test_rope_vs_validator_double_ref(oracle, heads, hd, pos, eps, seed):
+    """tools/v_rmsnorm_validate.cpp:67-83 cases against the double reference (tools/kt_utils.h:460-485),
+    tolerance 1e-3 as the reference validator; also within 2e-5 absolute (outputs are O(1))."""
+    buf = C.validator_row(seed, heads * hd).reshape(1, heads, hd)
+    w = C.validator_weight(seed + 1, hd)
+    ct, st = C.validator_rope_tables(pos, hd, hd)
+    got = oracle.rmsnorm_rope(buf, w, ct, st, np.array([pos], np.int32), eps)
+    ref = oracle.rmsnorm_rope_double_ref(buf, w, ct, st, [pos], eps)
+    assert np.max(np.abs(got - ref)) < 1e-3
+    b = buf.astype(np.float64)
+    sc = 1.0 / np.sqrt(np.mean(b * b, axis=-1, keepdims=True) + eps)
+    xn = b * sc * w
+    h = hd // 2
+    c = ct[pos, :h].astype(np.float64)
+    s = st[pos, :h].astype(np.float64)
+    d = np.concatenate([xn[..., :h] * c - xn[..., h:] * s, xn[..., :h] * s + xn[..., h:] * c], axis=-1)
+    assert np.max(np.abs(got - d)) < 2e-5
+
+
+def test_rope_tables_vs_double(oracle):
+    """freq_j = base^(-j/half), cos/sin(pos*freq_j) rounded once to binary32: within 1 ulp of numpy double."""
+    P, D, base = 2048, 128, 1e6
+    c, s = oracle.rope_tables(P, D, base)
+    half = D // 2
+    f = np.power(np.float64(base), -np.arange(half, dtype=np.float64) / half)
+    ang = np.arange(P, dtype=np.float64)[:, None] * f[None, :]
+    dc, ds = np.cos(ang), np.sin(ang)
+    assert np.all(np.abs(c - dc) <= np.spacing(np.abs(dc).astype(F)) + 1e-12)
+    assert np.all(np.abs(s - ds) <= np.spacing(np.abs(ds).astype(F)) + 1e-12)
+    assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
+
+
+# --------------------------------------------------------------------------- sigmoid / SwiGLU (a5, a6, a8)
+
+def test_sigmoid_constants_and_special_values(oracle):
+    assert float(oracle.sigmoid(0.0)) == 0.5  # fx = 0: p = 1, e = 1, 1/(1+1)
+    assert float(oracle.sigmoid(100.0)) == 1.0  # clamped to -80: e = 2^-115.4.., 1/(1+e) rounds to 1
+    lo = float(oracle.sigmoid(-100.0))  # clamped to 80: 1/(1+e^80)
+    assert abs(lo - math.exp(-80.0)) / math.exp(-80.0) < 1e-6
+    # vmaxps(NaN, -80) returns -80: a NaN gate clamps to x = -80, i.e. sigmoid 1 (then NaN * 1 in SwiGLU)
+    assert float(oracle.sigmoid(float("nan"))) == 1.0
+
+
+def test_sigmoid_dense_sweep_vs_double(oracle):
+    """The degree-5 exp2 polynomial is stated at 1.27e-7 max relative error (src/asm/v7_macros.inc:127-128).
+    With the roundings around it the sigmoid stays within 5e-7 relative of double, plus the error that the
+    rounding of fx = -g*log2e carries into 2^fx for g < 0 (half an ulp of |fx|, times ln 2: about
+    6e-8 * |g|).  A wrong coefficient or a misplaced Horner operand breaks this by orders of magnitude."""
+    g = np.linspace(-80.0, 30.0, 400001).astype(F)
+    got = np.array([oracle.sigmoid(float(v)) for v in g[::7]], np.float64)
+    gd = g[::7].astype(np.float64)
+    ref = 1.0 / (1.0 + np.exp(-gd))
+    rel = np.abs(got - ref) / ref
+    assert np.all(rel < 5e-7 + 7e-8 * np.maximum(-gd, 0.0))
+    assert np.max(rel[gd > -4]) < 5e-7
+
+
+def test_swiglu_vs_double(oracle):
+    g = C.normal(301, 200000, 1.5)
+    u = C.normal(302, 200000, 1.5)
+    got = oracle.swiglu(g, u).astype(np.float64)
+    ref = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64))) * u
+    m = np.abs(ref) > 1e-30
+    assert np.max(np.abs(got - ref)[m] / np.abs(ref)[m]) < 1e-5
+    # u = 1 leaves silu(g) = sigmoid(g)*g, one binary32 multiply after the sigmoid
+    gs = C.normal(7, 1000, 1.5)
+    sil = np.array([np.float32(oracle.sigmoid(float(v))) * v for v in gs], F)
+    assert bits_equal(oracle.swiglu(gs, np.ones_like(gs)), sil)
+
+
+# --------------------------------------------------------------------------- quantize (a7) and SwiGLU -> Q8 (a8)
+
+def test_quantizer_floor_constant():
+    """scalar_epsilon = 127 * 2^-126 (src/asm/quantize_kernel.inc:40-41): its /127 is exactly 2^-126."""
+    fl = np.float32(1.4928778e-36)
+    assert fl == np.float32(127.0) * np.float32(2.0 ** -126)
+    assert fl / np.float32(127.0) == np.float32(2.0 ** -126)
+
+
+@pytest.mark.parametrize("pattern", C.KT_PATTERNS)
+@pytest.mark.parametrize("n", [64, 256, 1024, 4096, 8192, 65536])
+def test_quantize_vs_kt_quantize_c_ref(oracle, pattern, n):
+    """tools/v_quantize_validate.cpp: 7 patterns x sizes x seeds {12345, 67890, 11111}; int8 codes must equal
+    kt_quantize_c_ref's exactly; scales equal except the all-zero group (1/127 there, 2^-126 in the kernel)."""
+    for seed in (12345, 67890, 11111):
+        x = C.kt_pattern(pattern, n, seed)
+        q, s = oracle.quantize(x[None], 64)
+        kq, ks = oracle.kt_quantize_c_ref(x)
+        assert bits_equal(q[0], kq), pattern
+        nz = np.max(np.abs(x.reshape(-1, 64)), axis=1) > 0
+        assert bits_equal(s[0][nz], ks[nz])
+        assert np.all(s[0][~nz] == np.float32(2.0 ** -126))
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_quantize_closed_form_properties(oracle, gs):
+    x = C.normal(9, (37, 1024), 2.0)
+    x[3, :gs] = 0.0
+    q, s = oracle.quantize(x, gs)
+    xg = x.reshape(37, -1, gs).astype(np.float64)
+    qg = q.reshape(37, -1, gs).astype(np.float64)
+    amax = np.max(np.abs(xg), axis=-1)
+    assert np.all(s[amax > 0] == (amax[amax > 0] / 127.0).astype(F)) or np.allclose(
+        s[amax > 0], amax[amax > 0] / 127.0, rtol=6e-8)
+    # the group's largest magnitude maps to +-127; every code within half a step (plus rounding) of x/scale
+    assert np.all(np.max(np.abs(qg), axis=-1)[amax > 0] == 127)
+    err = np.abs(xg - qg * s[..., None].astype(np.float64))
+    assert np.all(err <= 0.5 * s[..., None] * (1 + 1e-5))
+    assert np.all(qg[3, 0] == 0) and s[3, 0] == np.float32(2.0 ** -126)
+    assert q.min() >= -127
+
+
+def test_quantize_tail_group(oracle):
+    """n % gs != 0: the last, partial group uses the scalar tail (quantize_kernel.inc:119-152) -- the same
+    values as quantizing that partial group on its own."""
+    x = C.normal(11, 100, 3.0)
+    q, s = oracle.quantize(x[None], 64)
+    q1, s1 = oracle.quantize(x[None, :64], 64)
+    q2, s2 = oracle.quantize(x[None, 64:], 64)
+    assert bits_equal(q[0], np.concatenate([q1[0], q2[0]]))
+    assert bits_equal(s[0], np.concatenate([s1[0], s2[0]]))
+    kq, _ = oracle.kt_quantize_c_ref(x)
+    assert bits_equal(q[0], kq)
+
+
+def test_swiglu_q8_is_quantize_of_swiglu_and_near_double(oracle):
+    g = C.normal(401, (16, 8192), 1.5)
+    u = C.normal(402, (16, 8192), 1.5)
+    for gs in (32, 64):
+        q, s = oracle.swiglu_q8(g, u, gs)
+        q2, s2 = oracle.quantize(oracle.swiglu(g, u), gs)
+        assert bits_equal(q, q2) and bits_equal(s, s2)
+        ref = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u).reshape(16, -1, gs)
+        ideal = ref / s[..., None].astype(np.float64)
+        assert np.max(np.abs(q.reshape(16, -1, gs) - ideal)) <= 0.5 + 1e-3
+
+
+# --------------------------------------------------------------------------- embedding dequant (a9)
+
+def test_embedding_closed_form(oracle):
+    """out[i] = (float)q[token*dim + i] * s[(token*dim)/64 + i/64] (src/asm/forward.inc:13-42): exact convert,
+    one binary32 multiply."""
+    vocab, dim = 300, 256
+    tq, ts = C.q8_table(21, vocab, dim)
+    ids = C.rng(22).integers(0, vocab, 50).astype(np.int32)
+    got = oracle.embedding_gather(ids, tq, ts, dim)
+    want = tq[ids].astype(F) * np.repeat(ts.reshape(vocab, dim // 64)[ids], 64, axis=1)
+    assert bits_equal(got, want.astype(F))
+
+
+# --------------------------------------------------------------------------- AVX2 restatement (CPU baseline)
+
+avx2 = pytest.mark.skipif("not __import__('oracle.oracle', fromlist=['x']).avx2_available()",
+                          reason="host CPU lacks AVX2/FMA")
+
+
+@avx2
+def test_avx2_matches_scalar_oracle(oracle):
+    r = C.normal(1, (8, 4096))
+    a = C.normal(2, (8, 4096))
+    w = C.norm_weight(3, 4096)
+    assert all(bits_equal(p, q) for p, q in zip(oracle.avx2_fused_add_rmsnorm_rows(r, a, w, 1e-6),
+                                                 oracle.fused_add_rmsnorm(r, a, w, 1e-6)))
+    for dim in (8, 24, 40, 72):
+        r2, a2, w2 = C.normal(dim, (3, dim)), C.normal(dim + 1, (3, dim)), C.norm_weight(dim, dim)
+        assert all(bits_equal(p, q) for p, q in zip(oracle.avx2_fused_add_rmsnorm_rows(r2, a2, w2, 1e-5),
+                                                     oracle.fused_add_rmsnorm(r2, a2, w2, 1e-5)))
+    x = C.normal(4, (16, 8, 128))
+    qw = C.norm_weight(5, 128)
+    ct, st = oracle.rope_tables(16, 128, 1e6)
+    pos = np.arange(16, dtype=np.int32)
+    assert bits_equal(oracle.avx2_rmsnorm_rope(x, qw, ct, st, pos, 1e-6), oracle.rmsnorm_rope(x, qw, ct, st, pos, 1e-6))
+    g = C.normal(6, 100003, 1.5)
+    u = C.normal(7, 100003, 1.5)
+    assert bits_equal(oracle.avx2_swiglu(g, u), oracle.swiglu(g, u))
+    xq = C.normal(8, (5, 8192 + 40), 2.0)
+    for gs in (32, 64):
+        assert all(bits_equal(p, q) for p, q in zip(oracle.avx2_quantize(xq, gs), oracle.quantize(xq, gs)))
+    tq, ts = C.q8_table(9, 100, 512)
+    ids = C.rng(10).integers(0, 100, 20).astype(np.int32)
+    assert bits_equal(oracle.avx2_embedding_gather(ids, tq, ts, 512), oracle.embedding_gather(ids, tq, ts, 512))
