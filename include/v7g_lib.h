@@ -133,6 +133,16 @@ int v7g_rope_init(int head_dim, float rope_base, int n_pos);
  * precision, then copied; synchronous). */
 int v7g_build_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base);
 
+/* Exhaustive self-check, on the current device, of the arithmetic identities
+ * the kernels rely on to reproduce the reference's IEEE divisions with shorter
+ * sequences: mismatches[0] = inputs d in [2^-126, 2^123) where rcp + one
+ * Newton step differs from 1.0f/d; mismatches[1] = finite x >= 127*2^-126
+ * where the fma-corrected x*(1/127) differs from x/127.0f; mismatches[2] =
+ * non-NaN g where the sigmoid differs from EVAL_SIGMOID with vdivps
+ * (src/asm/v7_macros.inc:98-160).  All three are 0 on a conforming device.
+ * Synchronous; allocates a 96 KiB device buffer.  No reference counterpart. */
+int v7g_arith_selfcheck(unsigned long long *mismatches);
+
 /* ---------------------------------------------------------------------------
  * 3. Batched entries (performance path)
  * ------------------------------------------------------------------------- */
@@ -172,8 +182,9 @@ int v7g_swiglu_q8(int8_t *out_q, float *out_s, const float *gate, const float *u
 int v7g_quantize_q8(int8_t *out_q, float *out_s, const float *x, int rows, int row_len, int gs);
 
 /* Q8 embedding gather: out[t, :] = dequant(table row ids[t]) for n_tokens ids
- * (device int32).  table_q [vocab, dim] int8, table_s [vocab*dim/64] f32.  An id
- * outside [0, vocab) yields a zero row.  dim % 64 == 0. */
+ * (device int32).  table_q [vocab, dim] int8 (4-byte aligned), table_s
+ * [vocab*dim/64] f32, out 16-byte aligned.  An id outside [0, vocab) yields a
+ * zero row.  dim % 64 == 0. */
 int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const int8_t *table_q,
                             const float *table_s, int dim, int vocab);
 

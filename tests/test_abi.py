@@ -135,7 +135,8 @@ def test_embedding_rejects(L):
     assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE, FAKE, 100, 1000)[0] == 2  # dim % 64
     assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE, FAKE, 128, 0)[0] == 2
     assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, None, 4, FAKE, FAKE, 128, 10)[0] == 1
-    assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE + 4, FAKE, 128, 10)[0] == 3
+    assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE + 2, FAKE, 128, 10)[0] == 3
+    assert _sticky(L, L.v7g_embedding_gather_q8, FAKE + 4, FAKE, 4, FAKE, FAKE, 128, 10)[0] == 3
 
 
 def test_sticky_error_keeps_the_first_code(L):

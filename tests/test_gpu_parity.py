@@ -54,9 +54,24 @@ def assert_bits(got, want, what=""):
                              f"got {got[tuple(idx[0])]!r} want {want[tuple(idx[0])]!r}")
 
 
+# --------------------------------------------------------------------------- arithmetic identities
+
+def test_arith_selfcheck_exhaustive(ops):
+    """rcp + Newton == 1/d, fma-corrected x/127 == IEEE x/127, and the sigmoid with both == EVAL_SIGMOID with
+    vdivps, each over its whole input range of binary32 patterns on this device."""
+    import ctypes
+
+    from v7multiplikator_amd import _lib
+    counts = (ctypes.c_ulonglong * 3)()
+    rc = _lib.load().v7g_arith_selfcheck(ctypes.addressof(counts))
+    assert rc == 0
+    assert list(counts) == [0, 0, 0]
+
+
 # --------------------------------------------------------------------------- embedding gather (a9)
 
-@pytest.mark.parametrize("vocab,dim,n", [(1000, 64, 7), (512, 128, 33), (3000, 1024, 100), (4096, 4096, 257)])
+@pytest.mark.parametrize("vocab,dim,n", [(1000, 64, 7), (512, 128, 33), (3000, 1024, 100), (4096, 4096, 257),
+                                         (700, 1088, 19), (900, 3072, 41)])
 def test_embedding_gather_matches_oracle(ops, oracle, vocab, dim, n):
     tq, ts = C.q8_table(11, vocab, dim)
     ids = C.rng(12).integers(0, vocab, n).astype(np.int32)

@@ -39,6 +39,7 @@ SIGNATURES = {
     "v7g_get_rope_tables": (_i, [_vp, _vp, _vp, _vp]),
     "v7g_rope_init": (_i, [_i, _f, _i]),
     "v7g_build_rope_tables": (_i, [_vp, _vp, _i, _i, _f]),
+    "v7g_arith_selfcheck": (_i, [_vp]),
     "v7g_fused_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
     "v7g_rmsnorm_rope_heads": (_i, [_vp, _i, _ll, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _f]),
     "v7g_qk_rmsnorm_rope": (_i, [_vp, _ll, _i, _vp, _vp, _ll, _i, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _i, _f]),

@@ -11,14 +11,16 @@
 //             out_j = fma(-xo, sin_j, xe*cos_j), out_{j+h} = fma(xo, cos_j, xe*sin_j).
 // cos/sin rows are table + pos*rope_max_dim.
 //
-// gfx950 layout: 8 lanes per head, 8 heads per wave.  Lane m of a head holds
-// the float4 at x[4m + 32k] for every 32-element block k, so each of the 32
-// FMA chains (YMM accumulator q, lane j <-> element 8q + j of every block) is
-// lane-local and runs in the reference order; the xor exchanges 2, 4, 1 are
-// exactly the (A+B)+(C+D) and HADD_YMM pairings.  When head_dim % 64 == 0 the
-// rotate-half partner of block k is block k + K/2 in the same lane, so the
-// rotation happens in registers; otherwise the normalised head goes through
-// LDS to meet its partner.  The result is bit-identical to the reference.
+// gfx950 layout: 8 lanes per head.  Lane m of a head holds the float4 at
+// x[4m + 32k] for every 32-element block k, so each of the 32 FMA chains (YMM
+// accumulator q, lane j <-> element 8q + j of every block) is lane-local and
+// runs in the reference order; the xor exchanges 2, 4, 1 are exactly the
+// (A+B)+(C+D) and HADD_YMM pairings.  When head_dim % 64 == 0 the rotate-half
+// partner of block k is block k + K/2 in the same lane, so the rotation
+// happens in registers and each 8-lane unit takes two heads (all loads of
+// both issued together); otherwise the normalised head goes through LDS to
+// meet its partner, one head per unit.  The result is bit-identical to the
+// reference.
 #include "v7g_device.h"
 #include "v7g_internal.h"
 
@@ -28,7 +30,7 @@ struct RopeArgs {
   RopeSide side[2];
   int n_sides;
   int heads_per_token;  // side[0].n_heads + side[1].n_heads
-  unsigned n_units;     // n_tokens * heads_per_token
+  unsigned n_heads;     // n_tokens * heads_per_token
   int head_dim;
   const float *cos_table;
   const float *sin_table;
@@ -39,30 +41,34 @@ struct RopeArgs {
   float eps;
 };
 
-template <int K, bool REG_ROTATE>
-__global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RopeArgs a) {
-  constexpr int HD = 32 * K;
-  __shared__ float lds[REG_ROTATE ? 1 : 32 * HD];  // 32 heads per block when rotating through LDS
-  const int m = threadIdx.x & 7;
-  const unsigned unit = (blockIdx.x * 256u + threadIdx.x) >> 3;
-  const bool live = unit < a.n_units;
-  const unsigned uu = live ? unit : 0u;
-  const unsigned t = uu / (unsigned)a.heads_per_token;
-  const int h = (int)(uu - t * (unsigned)a.heads_per_token);
+// Where head f (flat over tokens x heads) lives, its weights and position.
+struct HeadRef {
+  float *x;
+  const float *w;
+  int pos;
+  bool live;
+  bool bad_pos;
+};
+
+__device__ __forceinline__ HeadRef head_ref(const RopeArgs &a, unsigned f, int m) {
+  HeadRef r;
+  r.live = f < a.n_heads;
+  const unsigned ff = r.live ? f : 0u;
+  const unsigned t = ff / (unsigned)a.heads_per_token;
+  const int h = (int)(ff - t * (unsigned)a.heads_per_token);
   const int sd = (a.n_sides > 1 && h >= a.side[0].n_heads) ? 1 : 0;
   const int hs = h - (sd ? a.side[0].n_heads : 0);
-  float *x_ptr = a.side[sd].buf + (size_t)t * (size_t)a.side[sd].token_stride + (size_t)hs * HD + 4 * m;
-  const float *w_ptr = a.side[sd].norm_weight + 4 * m;
+  r.x = a.side[sd].buf + (size_t)t * (size_t)a.side[sd].token_stride + (size_t)hs * a.head_dim + 4 * m;
+  r.w = a.side[sd].norm_weight + 4 * m;
   int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
   // A position outside the tables cannot be read: its heads become NaN.
-  const bool bad_pos = pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
-  if (bad_pos) pos = 0;
+  r.bad_pos = pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
+  r.pos = r.bad_pos ? 0 : pos;
+  return r;
+}
 
-  float4 x[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k)
-    x[k] = live ? *reinterpret_cast<const float4 *>(x_ptr + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
-
+template <int K>
+__device__ __forceinline__ float head_scale(const float4 (&x)[K], int head_dim, float eps) {
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
@@ -81,81 +87,124 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RopeArgs a) {
   acc.z = acc.z + xor_f(acc.z, 1); acc.w = acc.w + xor_f(acc.w, 1);
   const float t0 = acc.x + acc.y;
   const float t2 = acc.z + acc.w;
-  const float ss = t0 + t2;
-  const float s = rms_scale(ss, (float)HD, a.eps);
+  return rms_scale(t0 + t2, (float)head_dim, eps);
+}
 
-  float4 xn[K];
+template <int K>
+__device__ __forceinline__ void normalise(float4 (&xn)[K], const float4 (&x)[K], const float *w_ptr, float s,
+                                          bool bad_pos) {
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    float4 w = *reinterpret_cast<const float4 *>(w_ptr + 32 * k);
+    const float4 w = *reinterpret_cast<const float4 *>(w_ptr + 32 * k);
     xn[k] = make_float4((x[k].x * s) * w.x, (x[k].y * s) * w.y, (x[k].z * s) * w.z, (x[k].w * s) * w.w);
   }
-
   if (bad_pos) {
+    const float q = __builtin_nanf("");
 #pragma unroll
-    for (int k = 0; k < K; ++k) xn[k] = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+    for (int k = 0; k < K; ++k) xn[k] = make_float4(q, q, q, q);
   }
-  const size_t row = (size_t)pos * (size_t)a.rope_max_dim;
-  if constexpr (REG_ROTATE) {
-    if (pos != 0) {
-      const float *cr = a.cos_table + row + 4 * m;
-      const float *sr = a.sin_table + row + 4 * m;
-      constexpr int KH = K / 2;
+}
+
+// head_dim % 64 == 0: HPU heads per 8-lane unit, rotation in registers.
+template <int K, int HPU>
+__global__ __launch_bounds__(256) void rmsnorm_rope_reg_kernel(RopeArgs a) {
+  constexpr int KH = K / 2;
+  const int m = threadIdx.x & 7;
+  const unsigned unit = (blockIdx.x * 256u + threadIdx.x) >> 3;
+  HeadRef hr[HPU];
+  float4 x[HPU][K];
 #pragma unroll
-      for (int k = 0; k < KH; ++k) {
-        float4 c = *reinterpret_cast<const float4 *>(cr + 32 * k);
-        float4 sn = *reinterpret_cast<const float4 *>(sr + 32 * k);
-        float4 e = xn[k], od = xn[k + KH];
-        xn[k] = make_float4(__builtin_fmaf(-od.x, sn.x, e.x * c.x), __builtin_fmaf(-od.y, sn.y, e.y * c.y),
-                            __builtin_fmaf(-od.z, sn.z, e.z * c.z), __builtin_fmaf(-od.w, sn.w, e.w * c.w));
-        xn[k + KH] = make_float4(__builtin_fmaf(od.x, c.x, e.x * sn.x), __builtin_fmaf(od.y, c.y, e.y * sn.y),
-                                 __builtin_fmaf(od.z, c.z, e.z * sn.z), __builtin_fmaf(od.w, c.w, e.w * sn.w));
-      }
-    }
-  } else {
-    // The partner of element e is e +- HD/2, in another lane: every head of
-    // the block (32 of them, HD floats each) goes through LDS.  All threads
-    // reach the barrier; the rotation itself is skipped at pos 0.
-    float *hb = lds + (threadIdx.x >> 3) * HD;
+  for (int e = 0; e < HPU; ++e) {
+    hr[e] = head_ref(a, unit * HPU + e, m);
 #pragma unroll
-    for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(hb + 4 * m + 32 * k) = xn[k];
-    __syncthreads();
-    if (pos != 0) {
-      constexpr int HALF = HD / 2;
+    for (int k = 0; k < K; ++k)
+      x[e][k] = hr[e].live ? *reinterpret_cast<const float4 *>(hr[e].x + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int e = 0; e < HPU; ++e) {
+    const float s = head_scale<K>(x[e], 32 * K, a.eps);
+    float4 xn[K];
+    normalise<K>(xn, x[e], hr[e].w, s, hr[e].bad_pos);
+    if (hr[e].pos != 0) {
+      const size_t row = (size_t)hr[e].pos * (size_t)a.rope_max_dim + 4 * m;
       const float *cr = a.cos_table + row;
       const float *sr = a.sin_table + row;
 #pragma unroll
-      for (int k = 0; k < K; ++k) {
-        float cur[4] = {xn[k].x, xn[k].y, xn[k].z, xn[k].w};
-        float out[4];
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) {
-          const int e = 4 * m + 32 * k + c4;
-          if (e < HALF) {
-            out[c4] = __builtin_fmaf(-hb[e + HALF], sr[e], cur[c4] * cr[e]);
-          } else {
-            const int j = e - HALF;
-            out[c4] = __builtin_fmaf(cur[c4], cr[j], hb[j] * sr[j]);
-          }
-        }
-        xn[k] = make_float4(out[0], out[1], out[2], out[3]);
+      for (int k = 0; k < KH; ++k) {
+        const float4 c = *reinterpret_cast<const float4 *>(cr + 32 * k);
+        const float4 sn = *reinterpret_cast<const float4 *>(sr + 32 * k);
+        const float4 ev = xn[k], od = xn[k + KH];
+        xn[k] = make_float4(__builtin_fmaf(-od.x, sn.x, ev.x * c.x), __builtin_fmaf(-od.y, sn.y, ev.y * c.y),
+                            __builtin_fmaf(-od.z, sn.z, ev.z * c.z), __builtin_fmaf(-od.w, sn.w, ev.w * c.w));
+        xn[k + KH] = make_float4(__builtin_fmaf(od.x, c.x, ev.x * sn.x), __builtin_fmaf(od.y, c.y, ev.y * sn.y),
+                                 __builtin_fmaf(od.z, c.z, ev.z * sn.z), __builtin_fmaf(od.w, c.w, ev.w * sn.w));
       }
     }
-  }
-
-  if (live) {
+    if (hr[e].live) {
 #pragma unroll
-    for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(x_ptr + 32 * k) = xn[k];
+      for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(hr[e].x + 32 * k) = xn[k];
+    }
+  }
+}
+
+// head_dim % 64 == 32: the partner of element e is e +- HD/2, in another lane;
+// every head of the block (32 of them, HD floats each) goes through LDS.  All
+// threads reach the barrier; the rotation itself is skipped at pos 0.
+template <int K>
+__global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
+  constexpr int HD = 32 * K;
+  constexpr int HALF = HD / 2;
+  __shared__ float lds[32 * HD];
+  const int m = threadIdx.x & 7;
+  const unsigned unit = (blockIdx.x * 256u + threadIdx.x) >> 3;
+  const HeadRef hr = head_ref(a, unit, m);
+  float4 x[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    x[k] = hr.live ? *reinterpret_cast<const float4 *>(hr.x + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+  const float s = head_scale<K>(x, HD, a.eps);
+  float4 xn[K];
+  normalise<K>(xn, x, hr.w, s, hr.bad_pos);
+  float *hb = lds + (threadIdx.x >> 3) * HD;
+#pragma unroll
+  for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(hb + 4 * m + 32 * k) = xn[k];
+  __syncthreads();
+  if (hr.pos != 0) {
+    const size_t row = (size_t)hr.pos * (size_t)a.rope_max_dim;
+    const float *cr = a.cos_table + row;
+    const float *sr = a.sin_table + row;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float cur[4] = {xn[k].x, xn[k].y, xn[k].z, xn[k].w};
+      float res[4];
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        const int e = 4 * m + 32 * k + c4;
+        if (e < HALF) {
+          res[c4] = __builtin_fmaf(-hb[e + HALF], sr[e], cur[c4] * cr[e]);
+        } else {
+          const int j = e - HALF;
+          res[c4] = __builtin_fmaf(cur[c4], cr[j], hb[j] * sr[j]);
+        }
+      }
+      xn[k] = make_float4(res[0], res[1], res[2], res[3]);
+    }
+  }
+  if (hr.live) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(hr.x + 32 * k) = xn[k];
   }
 }
 
 template <int K>
 static void launch_k(const RopeArgs &a, hipStream_t stream) {
-  unsigned blocks = (a.n_units + 31u) / 32u;
-  if ((32 * K) % 64 == 0)
-    hipLaunchKernelGGL((rmsnorm_rope_kernel<K, true>), dim3(blocks), dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL((rmsnorm_rope_kernel<K, false>), dim3(blocks), dim3(256), 0, stream, a);
+  if ((32 * K) % 64 == 0) {
+    constexpr int HPU = 2;
+    const unsigned units = (a.n_heads + HPU - 1) / HPU;
+    hipLaunchKernelGGL((rmsnorm_rope_reg_kernel<K, HPU>), dim3((units + 31u) / 32u), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((rmsnorm_rope_lds_kernel<K>), dim3((a.n_heads + 31u) / 32u), dim3(256), 0, stream, a);
+  }
 }
 
 void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int head_dim, const float *cos_table,
@@ -166,7 +215,7 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.side[0] = sides[0];
   a.side[1] = n_sides > 1 ? sides[1] : sides[0];
   a.heads_per_token = sides[0].n_heads + (n_sides > 1 ? sides[1].n_heads : 0);
-  a.n_units = (unsigned)n_tokens * (unsigned)a.heads_per_token;
+  a.n_heads = (unsigned)n_tokens * (unsigned)a.heads_per_token;
   a.head_dim = head_dim;
   a.cos_table = cos_table;
   a.sin_table = sin_table;

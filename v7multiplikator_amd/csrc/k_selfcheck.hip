@@ -1,0 +1,99 @@
+// k_selfcheck.hip -- exhaustive check, on the running device, of the three
+// arithmetic identities the hot kernels rely on (v7g_device.h):
+//   0. rcp_rn(d) == 1.0f / d          for every d in [2^-126, 2^123)
+//   1. div127_rn(x) == x / 127.0f     for every finite x >= 127 * 2^-126
+//   2. sigmoid_v7(g) == the same sequence with max/min clamp and IEEE
+//      division (EVAL_SIGMOID as written, src/asm/v7_macros.inc:98-160) for
+//      every non-NaN binary32 g.
+// Each case walks its whole range of bit patterns (about 2^31, 2^31 and 2^32
+// values), a few milliseconds of GPU time.  Results are per-block counts in
+// caller-visible device memory, summed on the host.
+#include <vector>
+
+#include "v7g_device.h"
+#include "v7g_internal.h"
+
+namespace v7g {
+
+// EVAL_SIGMOID with the reference's operations one for one: vmaxps/vminps
+// clamp and vdivps.
+__device__ __forceinline__ float sigmoid_ieee(float g) {
+  const float log2e = 1.4426950408889634f;
+  float x = -g;
+  x = __builtin_fmaxf(x, -80.0f);
+  x = __builtin_fminf(x, 80.0f);
+  float fx = x * log2e;
+  float ip = __builtin_rintf(fx);
+  float fp = fx - ip;
+  float p = bits_f(0x3AADD303u);
+  p = __builtin_fmaf(fp, p, bits_f(0x3C1E7411u));
+  p = __builtin_fmaf(fp, p, bits_f(0x3D635B9Bu));
+  p = __builtin_fmaf(fp, p, bits_f(0x3E75FCE0u));
+  p = __builtin_fmaf(fp, p, bits_f(0x3F317215u));
+  p = __builtin_fmaf(fp, p, 1.0f);
+  float e = __builtin_ldexpf(p, (int)ip);
+  return 1.0f / (e + 1.0f);
+}
+
+constexpr int kCheckBlocks = 4096;
+
+__global__ __launch_bounds__(256) void arith_check_kernel(int which, uint64_t lo, uint64_t count,
+                                                          unsigned long long *block_counts) {
+  __shared__ unsigned long long part[256];
+  unsigned long long bad = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < count; i += stride) {
+    const float v = bits_f((uint32_t)(lo + i));
+    float fast, exact;
+    if (which == 0) {
+      fast = rcp_rn(v);
+      exact = 1.0f / v;
+    } else if (which == 1) {
+      fast = div127_rn(v);
+      exact = v / 127.0f;
+    } else {
+      if (v != v) continue;
+      fast = sigmoid_v7(v);
+      exact = sigmoid_ieee(v);
+    }
+    bad += __builtin_bit_cast(uint32_t, fast) != __builtin_bit_cast(uint32_t, exact);
+  }
+  part[threadIdx.x] = bad;
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if (threadIdx.x < h) part[threadIdx.x] += part[threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) block_counts[blockIdx.x] = part[0];
+}
+
+int arith_selfcheck(unsigned long long mismatches[3], hipStream_t stream) {
+  struct Range {
+    uint64_t lo, hi;
+  };
+  const Range ranges[3] = {{0x00800000ull, 0x7D000000ull},    // [2^-126, 2^123)
+                           {0x03FE0000ull, 0x7F800000ull},    // [127*2^-126, Inf)
+                           {0x00000000ull, 0x100000000ull}};  // every pattern (NaNs skipped)
+  unsigned long long *d = nullptr;
+  if (hipMalloc(&d, sizeof(unsigned long long) * kCheckBlocks * 3) != hipSuccess) return -1;
+  for (int w = 0; w < 3; ++w)
+    hipLaunchKernelGGL(arith_check_kernel, dim3(kCheckBlocks), dim3(256), 0, stream, w, ranges[w].lo,
+                       ranges[w].hi - ranges[w].lo, d + (size_t)w * kCheckBlocks);
+  std::vector<unsigned long long> h((size_t)kCheckBlocks * 3);
+  int rc = 0;
+  if (hipGetLastError() != hipSuccess ||
+      hipMemcpyAsync(h.data(), d, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost, stream) !=
+          hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    rc = -1;
+  (void)hipFree(d);
+  if (rc) return rc;
+  for (int w = 0; w < 3; ++w) {
+    unsigned long long t = 0;
+    for (int b = 0; b < kCheckBlocks; ++b) t += h[(size_t)w * kCheckBlocks + b];
+    mismatches[w] = t;
+  }
+  return 0;
+}
+
+}  // namespace v7g

@@ -13,38 +13,36 @@
 // The reference group size is 64 (src/asm/v7_core.inc:120); GS is a template
 // parameter so 32-element blocks use the same algorithm.
 //
-// Vector layout: lane owns 4 consecutive floats (dwordx4 loads of gate and up
-// or x), GS/4 consecutive lanes form one group, the group max is a DPP
-// butterfly inside 8 or 16 lanes, each lane stores its 4 codes as one dword,
-// and the first lane of the group stores the scale.
+// Vector layout: lane owns 4 consecutive floats (nontemporal dwordx4 loads of
+// gate and up, or x), GS/4 consecutive lanes form one group, the group max is
+// a DPP butterfly inside 8 or 16 lanes, each lane stores its 4 codes as one
+// dword, and the first lane of the group stores the scale.  The divisions of
+// the reference (sigmoid's 1/(1+e), wmax/127, 1/scale) are the shorter
+// sequences of v7g_device.h that give the same bits for every reachable input.
 #include "v7g_device.h"
 #include "v7g_internal.h"
 
 namespace v7g {
 
-constexpr int kSwigluU = 4;  // float4 chunks per thread in flight
-constexpr int kQuantU = 4;
+// One float4 chunk per thread and a grid that covers the array once: a
+// thread's loads are issued together and many waves keep them in flight.  The
+// grid-stride loop only runs more than once past 2^30 chunks.
+constexpr unsigned kStreamBlock = 256;
+constexpr long long kMaxStreamBlocks = 1ll << 22;
 
-__global__ __launch_bounds__(256) void swiglu_f32_kernel(float *out, const float *gate, const float *up, long long n4) {
-  const long long base = (long long)blockIdx.x * (256 * kSwigluU) + threadIdx.x;
-  const float4 *g4 = reinterpret_cast<const float4 *>(gate);
-  const float4 *u4 = reinterpret_cast<const float4 *>(up);
-  float4 *o4 = reinterpret_cast<float4 *>(out);
-  float4 g[kSwigluU], u[kSwigluU];
-#pragma unroll
-  for (int k = 0; k < kSwigluU; ++k) {
-    long long c = base + k * 256;
-    if (c < n4) {
-      g[k] = g4[c];
-      u[k] = u4[c];
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < kSwigluU; ++k) {
-    long long c = base + k * 256;
-    if (c < n4)
-      o4[c] = make_float4(swiglu_v7(g[k].x, u[k].x), swiglu_v7(g[k].y, u[k].y), swiglu_v7(g[k].z, u[k].z),
-                          swiglu_v7(g[k].w, u[k].w));
+static unsigned stream_blocks(long long n4) {
+  long long b = (n4 + kStreamBlock - 1) / kStreamBlock;
+  return (unsigned)(b < kMaxStreamBlocks ? b : kMaxStreamBlocks);
+}
+
+__global__ __launch_bounds__(kStreamBlock) void swiglu_f32_kernel(float *out, const float *gate, const float *up,
+                                                                  long long n4) {
+  const long long stride = (long long)gridDim.x * kStreamBlock;
+  for (long long c = (long long)blockIdx.x * kStreamBlock + threadIdx.x; c < n4; c += stride) {
+    const float4 g = ld_stream4(gate + 4 * c);
+    const float4 u = ld_stream4(up + 4 * c);
+    reinterpret_cast<float4 *>(out)[c] =
+        make_float4(swiglu_v7(g.x, u.x), swiglu_v7(g.y, u.y), swiglu_v7(g.z, u.z), swiglu_v7(g.w, u.w));
   }
 }
 
@@ -56,61 +54,45 @@ __global__ void swiglu_f32_tail_kernel(float *out, const float *gate, const floa
 
 void launch_swiglu_f32(float *out, const float *gate, const float *up, long long n, hipStream_t stream) {
   long long n4 = n / 4;
-  if (n4 > 0) {
-    long long blocks = (n4 + 256 * kSwigluU - 1) / (256 * kSwigluU);
-    hipLaunchKernelGGL(swiglu_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, out, gate, up, n4);
-  }
+  if (n4 > 0)
+    hipLaunchKernelGGL(swiglu_f32_kernel, dim3(stream_blocks(n4)), dim3(kStreamBlock), 0, stream, out, gate, up, n4);
   if (n % 4)
     hipLaunchKernelGGL(swiglu_f32_tail_kernel, dim3(1), dim3(4), 0, stream, out, gate, up, n4 * 4, n);
 }
 
 // Flat path: every row length is a multiple of GS, so groups tile the flat
-// array and group g covers elements [g*GS, (g+1)*GS).
+// array and group g covers elements [g*GS, (g+1)*GS).  GS/4 consecutive lanes
+// hold one group (8 or 16 lanes, aligned inside the wave, so a group never
+// straddles two waves or two loop iterations); their max is a DPP butterfly.
 template <int GS, bool SWIGLU>
-__global__ __launch_bounds__(256) void quantize_q8_flat_kernel(int8_t *__restrict__ out_q, float *__restrict__ out_s,
-                                                               const float *__restrict__ x,
-                                                               const float *__restrict__ gate,
-                                                               const float *__restrict__ up, long long n4) {
+__global__ __launch_bounds__(kStreamBlock) void quantize_q8_flat_kernel(int8_t *__restrict__ out_q,
+                                                                        float *__restrict__ out_s,
+                                                                        const float *__restrict__ x,
+                                                                        const float *__restrict__ gate,
+                                                                        const float *__restrict__ up, long long n4) {
   constexpr int LPG = GS / 4;  // lanes per group
-  const long long base = (long long)blockIdx.x * (256 * kQuantU) + threadIdx.x;
-  float4 v[kQuantU];
-#pragma unroll
-  for (int k = 0; k < kQuantU; ++k) {
-    long long c = base + k * 256;
-    if (c < n4) {
-      if constexpr (SWIGLU) {
-        float4 g = reinterpret_cast<const float4 *>(gate)[c];
-        float4 u = reinterpret_cast<const float4 *>(up)[c];
-        v[k] = make_float4(g.x, g.y, g.z, g.w);
-        v[k].x = swiglu_v7(g.x, u.x);
-        v[k].y = swiglu_v7(g.y, u.y);
-        v[k].z = swiglu_v7(g.z, u.z);
-        v[k].w = swiglu_v7(g.w, u.w);
-      } else {
-        v[k] = reinterpret_cast<const float4 *>(x)[c];
-      }
+  const long long stride = (long long)gridDim.x * kStreamBlock;
+  for (long long c = (long long)blockIdx.x * kStreamBlock + threadIdx.x; c < n4; c += stride) {
+    float4 v;
+    if constexpr (SWIGLU) {
+      const float4 g = ld_stream4(gate + 4 * c);
+      const float4 u = ld_stream4(up + 4 * c);
+      v = make_float4(swiglu_v7(g.x, u.x), swiglu_v7(g.y, u.y), swiglu_v7(g.z, u.z), swiglu_v7(g.w, u.w));
     } else {
-      v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      v = ld_stream4(x + 4 * c);
     }
-  }
-#pragma unroll
-  for (int k = 0; k < kQuantU; ++k) {
-    const long long c = base + k * 256;
-    float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v[k].x), __builtin_fabsf(v[k].y)),
-                              __builtin_fmaxf(__builtin_fabsf(v[k].z), __builtin_fabsf(v[k].w)));
+    // absmax (vandps + vmaxps tree, order-free for non-NaN input)
+    float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                              __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
     m = (LPG == 8) ? group8_max(m) : group16_max(m);
     float scale, recip;
     q8_scale(m, scale, recip);
-    if (c < n4) {
-      uint32_t packed = pack4_i8(q8_code(v[k].x * recip), q8_code(v[k].y * recip), q8_code(v[k].z * recip),
-                                 q8_code(v[k].w * recip));
-      reinterpret_cast<uint32_t *>(out_q)[c] = packed;
-      if ((threadIdx.x & (LPG - 1)) == 0) out_s[c / LPG] = scale;
-    }
+    reinterpret_cast<uint32_t *>(out_q)[c] = pack4_codes(v, recip);
+    if ((threadIdx.x & (LPG - 1)) == 0) out_s[c / LPG] = scale;
   }
 }
 
-// General path: any row length, any GS in [4, 256]; one thread per group,
+// General path: any row length, any GS in [1, 4096]; one thread per group,
 // scalar loads.  A partial last group of a row takes the reference's scalar
 // tail arithmetic (quantize_kernel.inc:119-152), value-identical to the
 // vector path for every non-NaN input.
@@ -128,8 +110,7 @@ __global__ __launch_bounds__(256) void quantize_q8_generic_kernel(int8_t *out_q,
   float wmax = 0.0f;
   for (int i = 0; i < len; ++i) {
     float v = SWIGLU ? swiglu_v7(gate[start + i], up[start + i]) : x[start + i];
-    float a = __builtin_fabsf(v);
-    wmax = (a > wmax) ? a : wmax;
+    wmax = __builtin_fmaxf(wmax, __builtin_fabsf(v));
   }
   float scale, recip;
   q8_scale(wmax, scale, recip);
@@ -143,14 +124,14 @@ __global__ __launch_bounds__(256) void quantize_q8_generic_kernel(int8_t *out_q,
 template <int GS>
 static void launch_flat(int8_t *out_q, float *out_s, const float *x, const float *gate, const float *up, long long n,
                         hipStream_t stream) {
-  long long n4 = n / 4;
-  long long blocks = (n4 + 256 * kQuantU - 1) / (256 * kQuantU);
+  const long long n4 = n / 4;
+  const dim3 grid(stream_blocks(n4));
   if (gate)
-    hipLaunchKernelGGL((quantize_q8_flat_kernel<GS, true>), dim3((unsigned)blocks), dim3(256), 0, stream, out_q, out_s,
-                       x, gate, up, n4);
+    hipLaunchKernelGGL((quantize_q8_flat_kernel<GS, true>), grid, dim3(kStreamBlock), 0, stream, out_q, out_s, x, gate,
+                       up, n4);
   else
-    hipLaunchKernelGGL((quantize_q8_flat_kernel<GS, false>), dim3((unsigned)blocks), dim3(256), 0, stream, out_q,
-                       out_s, x, gate, up, n4);
+    hipLaunchKernelGGL((quantize_q8_flat_kernel<GS, false>), grid, dim3(kStreamBlock), 0, stream, out_q, out_s, x,
+                       gate, up, n4);
 }
 
 static bool aligned(const void *p, size_t a) { return p == nullptr || ((uintptr_t)p % a) == 0; }
@@ -159,7 +140,7 @@ void launch_quantize_q8(int8_t *out_q, float *out_s, const float *x, const float
                         int row_len, int gs, hipStream_t stream) {
   const long long n = (long long)rows * row_len;
   const bool flat = (gs == 32 || gs == 64) && row_len % gs == 0 && aligned(out_q, 4) && aligned(x, 16) &&
-                    aligned(gate, 16) && aligned(up, 16) && n / 4 < (1LL << 40);
+                    aligned(gate, 16) && aligned(up, 16);
   if (flat) {
     if (gs == 32)
       launch_flat<32>(out_q, out_s, x, gate, up, n, stream);

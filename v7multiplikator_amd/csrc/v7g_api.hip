@@ -63,6 +63,11 @@ int check_rope_common(int n_tokens, int head_dim, const float *cos_table, const 
   return V7G_OK;
 }
 
+// 8 lanes per head: the grid of n_tokens * heads_per_token heads must stay below 2^32 threads.
+int check_rope_heads(int n_tokens, int heads_per_token) {
+  return (long long)n_tokens * heads_per_token >= (1LL << 28) ? V7G_ERR_SHAPE : V7G_OK;
+}
+
 int check_rope_side(const float *buf, long long token_stride, int n_heads, int head_dim, const float *w,
                     int n_tokens) {
   if (n_heads <= 0 || token_stride % 4 != 0) return V7G_ERR_SHAPE;
@@ -182,6 +187,11 @@ int v7g_rope_init(int head_dim, float rope_base, int n_pos) {
   return V7G_OK;
 }
 
+int v7g_arith_selfcheck(unsigned long long *mismatches) {
+  if (!mismatches) return fail(V7G_ERR_NULL);
+  return v7g::arith_selfcheck(mismatches, stream()) == 0 ? V7G_OK : fail(V7G_ERR_HIP);
+}
+
 int v7g_get_rope_tables(float **cos_table, float **sin_table, int *rope_max_dim, int *n_pos) {
   std::lock_guard<std::mutex> lk(g_rope_mu);
   if (!g_rope_cos) return fail(V7G_ERR_NO_TABLES);
@@ -208,6 +218,7 @@ int v7g_rmsnorm_rope_heads(float *buf, int n_tokens, long long token_stride, int
                            const int32_t *positions, int pos0, int rope_max_dim, int table_rows, float eps) {
   int rc = check_rope_common(n_tokens, head_dim, cos_table, sin_table, rope_max_dim, table_rows);
   if (!rc) rc = check_rope_side(buf, token_stride, n_heads, head_dim, norm_weight, n_tokens);
+  if (!rc) rc = check_rope_heads(n_tokens, n_heads);
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
@@ -224,6 +235,7 @@ int v7g_qk_rmsnorm_rope(float *q, long long q_token_stride, int n_q_heads, const
   int rc = check_rope_common(n_tokens, head_dim, cos_table, sin_table, rope_max_dim, table_rows);
   if (!rc) rc = check_rope_side(q, q_token_stride, n_q_heads, head_dim, q_norm_weight, n_tokens);
   if (!rc) rc = check_rope_side(k, k_token_stride, n_kv_heads, head_dim, k_norm_weight, n_tokens);
+  if (!rc) rc = check_rope_heads(n_tokens, n_q_heads + n_kv_heads);
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
@@ -274,10 +286,10 @@ int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const 
   if (n_tokens < 0 || dim <= 0 || dim % 64 != 0 || vocab <= 0) return fail(V7G_ERR_SHAPE);
   if (n_tokens == 0) return V7G_OK;
   if (!out || !ids || !table_q || !table_s) return fail(V7G_ERR_NULL);
-  if ((long long)n_tokens * (dim / 16) >= (1LL << 32)) return fail(V7G_ERR_SHAPE);
-  if (!al16(out) || !al16(table_q) || ((uintptr_t)table_s & 3u) || ((uintptr_t)ids & 3u))
+  // one 256-thread block per 1024 codes of a row; the grid must stay below 2^32 threads
+  if ((long long)n_tokens * ((dim / 4 + 255) / 256) >= (1LL << 24)) return fail(V7G_ERR_SHAPE);
+  if (!al16(out) || ((uintptr_t)table_q & 3u) || ((uintptr_t)table_s & 3u) || ((uintptr_t)ids & 3u))
     return fail(V7G_ERR_ALIGN);
-  if (n_tokens == 0) return V7G_OK;
   v7g::launch_embedding_gather(out, ids, n_tokens, table_q, table_s, dim, vocab, stream());
   return check_launch();
 }
@@ -322,7 +334,7 @@ V7_ABI void v7s_embedding_row(float *out, int token, int dim, v7g_q8_tensor *q_d
   size_t base = (size_t)token * (size_t)dim;
   const int8_t *q = reinterpret_cast<const int8_t *>(q_desc->q) + base;
   const float *s = q_desc->s + (base >> 6);
-  if (!al16(out) || !al16(q) || ((uintptr_t)s & 3u)) {
+  if (!al16(out) || ((uintptr_t)q & 3u) || ((uintptr_t)s & 3u)) {
     fail(V7G_ERR_ALIGN);
     return;
   }

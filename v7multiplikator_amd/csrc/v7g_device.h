@@ -5,7 +5,9 @@
 // sequence with one correctly rounded gfx950 operation per x86 operation.
 // The library is built with -ffp-contract=off, so `a * b + c` stays two
 // roundings and __builtin_fmaf is the only fused multiply-add; f32 division
-// and sqrt are the correctly rounded expansions (hipcc's default).
+// and sqrt are the correctly rounded expansions (hipcc's default).  The hot
+// loops replace two divisions by shorter sequences that give the same bits
+// for every input they can receive (rcp_rn, div127_rn below).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -15,21 +17,44 @@ namespace v7g {
 // EVAL_SIGMOID constants: src/asm/math_data.inc:16-53.
 __device__ __forceinline__ float bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
 
+// 1/d for d in [2^-126, 2^123): v_rcp_f32 (within 1 ulp) and one Newton step
+// with fused multiply-adds, e = fma(-d, r, 1) (exact), r + e*r.  For every d
+// in that range this equals the correctly rounded IEEE division 1.0f/d, bit
+// for bit; v7g_arith_selfcheck() verifies it exhaustively on the running
+// device.  Outside the range (0, Inf, subnormals) callers handle the value
+// themselves.
+__device__ __forceinline__ float rcp_rn(float d) {
+  float r = __builtin_amdgcn_rcpf(d);
+  float e = __builtin_fmaf(-d, r, 1.0f);
+  return __builtin_fmaf(e, r, r);
+}
+
+// x / 127 correctly rounded, for finite x >= 127*2^-126: q0 = x*RN(1/127),
+// the remainder x - 127*q0 is exact in one fma, and one more fma corrects q0.
+// Equal to the IEEE division for every such x (exhaustively checked by
+// v7g_arith_selfcheck()).
+__device__ __forceinline__ float div127_rn(float x) {
+  const float inv = 1.0f / 127.0f;
+  float q0 = x * inv;
+  float r = __builtin_fmaf(-q0, 127.0f, x);
+  return __builtin_fmaf(r, inv, q0);
+}
+
 // EVAL_SIGMOID, packed form (src/asm/v7_macros.inc:98-160):
 //   x = clamp(-g, -80, 80); fx = x*log2e; i = rne(fx); f = fx - i;
 //   p = C5; p = fma(f,p,C4) ... fma(f,p,C1); p = fma(f,p,1); e = 2^i * p;
 //   sigma = 1 / (1 + e).
-// 2^i * p is formed with v_ldexp_f32: the reference multiplies p by the
-// exact power of two built from exponent bits, and that product is exact for
-// the reachable range (|i| <= 116, p in [0.7, 1.42]), so ldexp gives the same
-// bits in one instruction.  The clamp uses max/min: identical to x86
-// vmaxps/vminps for every non-NaN input; a NaN gate makes the SwiGLU product
-// NaN on both sides whatever the clamp returns.
+// The clamp is one v_med3_f32 (max then min for every non-NaN input; a NaN
+// gate makes the SwiGLU product NaN on both sides whatever the clamp returns).
+// 2^i * p is formed with v_ldexp_f32: the reference multiplies p by the exact
+// power of two built from exponent bits, and that product is exact for the
+// reachable range (|i| <= 116, p in [0.7, 1.42]), so ldexp gives the same
+// bits.  1/(1+e) is rcp_rn: 1 + e lies in [1, 2^117).  The whole function
+// equals the same sequence with IEEE division for all 2^32 inputs
+// (v7g_arith_selfcheck()).
 __device__ __forceinline__ float sigmoid_v7(float g) {
   const float log2e = 1.4426950408889634f;
-  float x = -g;
-  x = __builtin_fmaxf(x, -80.0f);
-  x = __builtin_fminf(x, 80.0f);
+  float x = __builtin_amdgcn_fmed3f(-g, -80.0f, 80.0f);
   float fx = x * log2e;
   float ip = __builtin_rintf(fx);
   float fp = fx - ip;
@@ -40,8 +65,7 @@ __device__ __forceinline__ float sigmoid_v7(float g) {
   p = __builtin_fmaf(fp, p, bits_f(0x3F317215u));
   p = __builtin_fmaf(fp, p, 1.0f);
   float e = __builtin_ldexpf(p, (int)ip);
-  float d = e + 1.0f;
-  return 1.0f / d;
+  return rcp_rn(e + 1.0f);
 }
 
 // SwiGLU element, src/asm/prefill_q8.inc:1159-1165: (sigma(g) * g) * u.
@@ -54,30 +78,41 @@ __device__ __forceinline__ float swiglu_v7(float g, float u) {
 #define V7G_Q_FLOOR 1.4928778e-36f
 
 // Per-group scale and reciprocal, src/asm/quantize_kernel.inc:84-89:
-// wmax = max(wmax, floor); scale = wmax / 127; recip = 1 / scale.
+// wmax = max(wmax, floor); scale = wmax / 127; recip = 1 / scale.  An Inf
+// group max (an Inf input) gives scale Inf and recip 0, as IEEE division does.
 __device__ __forceinline__ void q8_scale(float wmax, float &scale, float &recip) {
-  wmax = (wmax > V7G_Q_FLOOR) ? wmax : V7G_Q_FLOOR;
-  scale = wmax / 127.0f;
-  recip = 1.0f / scale;
+  wmax = __builtin_fmaxf(wmax, V7G_Q_FLOOR);
+  const bool inf = wmax == __builtin_inff();
+  scale = inf ? wmax : div127_rn(wmax);
+  recip = inf ? 0.0f : rcp_rn(scale);
 }
 
-// One int8 code, src/asm/quantize_kernel.inc:91-105 (vmulps, vcvtps2dq,
-// signed-saturating packs, vpmaxsb -127): rne(x * recip) clamped to
-// [-127, 127]; a NaN product gives -127 (x86 converts NaN to 0x80000000,
-// which saturates to -128 and is raised to -127).  fmaxf returns the non-NaN
-// operand, so NaN lands on -127 here too.  |x * recip| <= 127.00002 for every
-// finite input, so the out-of-int32-range case of vcvtps2dq is unreachable.
-__device__ __forceinline__ int q8_code(float v) {
-  float r = __builtin_rintf(v);
-  r = __builtin_fmaxf(r, -127.0f);
-  r = __builtin_fminf(r, 127.0f);
-  return (int)r;
+// One int8 code as the low byte of its two's complement, src/asm/quantize_kernel.inc:91-105
+// (vmulps, vcvtps2dq, signed-saturating packs, vpmaxsb -127): rne(v)
+// clamped to [-127, 127], with v = x * recip.  For finite x, |v| <= 127.00002,
+// so only the lower clamp can bind; a NaN v must give -127 (x86 converts NaN
+// to 0x80000000, which saturates to -128 and is raised to -127), and
+// max(v, -127) returns -127 for NaN.  Adding 1.5*2^23 rounds v to an integer
+// with ties to even in the low mantissa bits, whose low byte is the code.
+__device__ __forceinline__ uint32_t q8_code_byte(float v) {
+  v = __builtin_fmaxf(v, -127.0f);
+  return __builtin_bit_cast(uint32_t, v + 12582912.0f) & 0xffu;
+}
+__device__ __forceinline__ int q8_code(float v) { return (int)(int8_t)q8_code_byte(v); }
+
+__device__ __forceinline__ uint32_t pack4_codes(float4 v, float recip) {
+  return q8_code_byte(v.x * recip) | (q8_code_byte(v.y * recip) << 8) | (q8_code_byte(v.z * recip) << 16) |
+         (q8_code_byte(v.w * recip) << 24);
 }
 
-__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
-  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-         ((uint32_t)(d & 0xff) << 24);
+// Streaming loads of data read exactly once (nontemporal: they do not displace
+// reused lines such as RoPE tables and norm weights from L2 and MALL).
+typedef float v7g_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_stream4(const float *p) {
+  v7g_f4 a = __builtin_nontemporal_load(reinterpret_cast<const v7g_f4 *>(p));
+  return make_float4(a.x, a.y, a.z, a.w);
 }
+__device__ __forceinline__ uint32_t ld_stream_u32(const uint32_t *p) { return __builtin_nontemporal_load(p); }
 
 // DPP lane exchanges inside a 16-lane row (gfx9 encodings).
 enum : int {

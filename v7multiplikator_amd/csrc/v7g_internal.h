@@ -31,4 +31,10 @@ void launch_swiglu_f32(float *out, const float *gate, const float *up, long long
 void launch_quantize_q8(int8_t *out_q, float *out_s, const float *x, const float *gate, const float *up, int rows,
                         int row_len, int gs, hipStream_t stream);
 
+// Exhaustive check of rcp_rn, div127_rn and sigmoid_v7 against IEEE division
+// on the current device (synchronous; allocates a small device buffer).
+// mismatches[i] = number of inputs where identity i fails; returns 0 or -1 on
+// a HIP error.
+int arith_selfcheck(unsigned long long mismatches[3], hipStream_t stream);
+
 }  // namespace v7g
