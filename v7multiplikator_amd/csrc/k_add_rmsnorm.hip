@@ -12,7 +12,8 @@
 // This kernel reproduces that order exactly, so its output is bit-identical.
 // One workgroup per row: each thread keeps its float4 chunks of the row in
 // registers (4*(tid + k*TPR) for k < KMAX), so pass 1 issues every load of
-// residual and add together and pass 2 needs no second read.  The updated
+// residual and add together and pass 2 needs no second read; residual, add
+// and o move as streaming loads and stores, the weight row stays cached.  The updated
 // residual also goes to LDS, where 32 lanes of wave 0 replay the 32 FMA
 // chains (lane 8q + j is accumulator q, YMM lane j), conflict-free; the
 // five-step xor exchange below is exactly the (A+B)+(C+D) + HADD_YMM pairing.
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(TPR) void fused_add_rmsnorm_kernel(float *o, float 
     const int i = 4 * (tid + k * TPR);
     if (i < dim) {
       x[k] = make_float4(x[k].x + b[k].x, x[k].y + b[k].y, x[k].z + b[k].z, x[k].w + b[k].w);
-      *reinterpret_cast<float4 *>(res + i) = x[k];
+      st_stream4(res + i, x[k]);
       *reinterpret_cast<float4 *>(row + i) = x[k];
     }
   }
@@ -91,8 +92,7 @@ __global__ __launch_bounds__(TPR) void fused_add_rmsnorm_kernel(float *o, float 
     const int i = 4 * (tid + k * TPR);
     if (i < dim) {
       const float4 w = *reinterpret_cast<const float4 *>(weight + i);
-      *reinterpret_cast<float4 *>(out + i) =
-          make_float4((s * x[k].x) * w.x, (s * x[k].y) * w.y, (s * x[k].z) * w.z, (s * x[k].w) * w.w);
+      st_stream4(out + i, make_float4((s * x[k].x) * w.x, (s * x[k].y) * w.y, (s * x[k].z) * w.z, (s * x[k].w) * w.w));
     }
   }
 }

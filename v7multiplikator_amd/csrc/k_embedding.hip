@@ -5,15 +5,20 @@
 // int8 -> f32 conversion followed by one multiply.  Here one launch gathers all
 // tokens of a batch; the result is bit-identical by construction.
 //
-// Layout: a 256-thread block covers 1024 codes (256 dwords) of one row; lane l
-// loads dword l of that stretch (four codes, one coalesced 1 KiB load per
-// wave) and its 64-code group's scale, and stores four floats (one coalesced
-// 4 KiB dwordx4 store per wave).  Rows of any dim % 64 == 0 take
-// ceil(dim/1024) blocks; a partial last block predicates its lanes.
+// Layout: a 256-thread block covers 4096 codes (1024 dwords) of one row; lane
+// l loads dwords l, l+256, l+512, l+768 of that stretch (four codes each, each
+// load one coalesced 1 KiB access per wave, all four issued before any
+// convert) with the 64-code group's scale, and stores four floats per dword
+// (coalesced 4 KiB dwordx4 stores per wave).  Codes and output stream past
+// the caches; the scales use ordinary loads.  Rows of any dim % 64 == 0 take
+// ceil(dim/4096) blocks; a partial last block clamps its loads and predicates
+// its stores.
 #include "v7g_device.h"
 #include "v7g_internal.h"
 
 namespace v7g {
+
+constexpr unsigned kEmbDwords = 4;  // dwords (4 codes each) per thread
 
 __global__ __launch_bounds__(256) void embedding_gather_q8_kernel(float *__restrict__ out,
                                                                   const int32_t *__restrict__ ids,
@@ -22,30 +27,45 @@ __global__ __launch_bounds__(256) void embedding_gather_q8_kernel(float *__restr
                                                                   const float *__restrict__ table_s, int dim,
                                                                   int vocab) {
   const unsigned t = blockIdx.x / blocks_per_row;
-  const unsigned w = (blockIdx.x - t * blocks_per_row) * 256u + threadIdx.x;  // dword of the row
-  const unsigned dw = (unsigned)dim >> 2;
-  if (w >= dw) return;
-  const int id = ids ? ids[t] : (int)t;  // no id array: row t of the table
-  float4 *dst = reinterpret_cast<float4 *>(out + (size_t)t * dim) + w;
+  const unsigned w0 = (blockIdx.x - t * blocks_per_row) * (256u * kEmbDwords) + threadIdx.x;
+  const unsigned dw = (unsigned)dim >> 2;  // dwords per row
+  const int id = ids ? ids[t] : (int)t;    // no id array: row t of the table
+  float *dst = out + (size_t)t * dim;
   if ((unsigned)id >= (unsigned)vocab) {
     // An id outside the table cannot be read; its row is written as zeros.
-    *dst = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (unsigned j = 0; j < kEmbDwords; ++j) {
+      const unsigned w = w0 + 256u * j;
+      if (w < dw) st_stream4(dst + 4 * w, make_float4(0.f, 0.f, 0.f, 0.f));
+    }
     return;
   }
   const size_t base = (size_t)id * (size_t)dim;
-  const uint32_t u = reinterpret_cast<const uint32_t *>(table_q + base)[w];
-  const float s = table_s[(base >> 6) + (w >> 4)];
-  float4 v;
-  v.x = (float)((int32_t)(u << 24) >> 24) * s;
-  v.y = (float)((int32_t)(u << 16) >> 24) * s;
-  v.z = (float)((int32_t)(u << 8) >> 24) * s;
-  v.w = (float)((int32_t)u >> 24) * s;
-  *dst = v;
+  const uint32_t *src = reinterpret_cast<const uint32_t *>(table_q + base);
+  const float *sc = table_s + (base >> 6);
+  uint32_t q[kEmbDwords];
+  float s[kEmbDwords];
+#pragma unroll
+  for (unsigned j = 0; j < kEmbDwords; ++j) {
+    const unsigned w = w0 + 256u * j;
+    const unsigned wc = w < dw ? w : dw - 1;
+    q[j] = ld_stream_u32(src + wc);
+    s[j] = sc[wc >> 4];
+  }
+#pragma unroll
+  for (unsigned j = 0; j < kEmbDwords; ++j) {
+    const unsigned w = w0 + 256u * j;
+    const uint32_t u = q[j];
+    const float4 v = make_float4((float)((int32_t)(u << 24) >> 24) * s[j], (float)((int32_t)(u << 16) >> 24) * s[j],
+                                 (float)((int32_t)(u << 8) >> 24) * s[j], (float)((int32_t)u >> 24) * s[j]);
+    if (w < dw) st_stream4(dst + 4 * w, v);
+  }
 }
 
 void launch_embedding_gather(float *out, const int32_t *ids, int n_tokens, const int8_t *table_q,
                              const float *table_s, int dim, int vocab, hipStream_t stream) {
-  const unsigned bpr = ((unsigned)dim / 4u + 255u) / 256u;
+  const unsigned per_block = 256u * kEmbDwords;
+  const unsigned bpr = ((unsigned)dim / 4u + per_block - 1u) / per_block;
   const unsigned blocks = (unsigned)n_tokens * bpr;
   hipLaunchKernelGGL(embedding_gather_q8_kernel, dim3(blocks), dim3(256), 0, stream, out, ids, bpr, table_q, table_s,
                      dim, vocab);

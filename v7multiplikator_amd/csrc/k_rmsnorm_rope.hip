@@ -17,9 +17,10 @@
 // runs in the reference order; the xor exchanges 2, 4, 1 are exactly the
 // (A+B)+(C+D) and HADD_YMM pairings.  When head_dim % 64 == 0 the rotate-half
 // partner of block k is block k + K/2 in the same lane, so the rotation
-// happens in registers and each 8-lane unit takes two heads (all loads of
-// both issued together); otherwise the normalised head goes through LDS to
-// meet its partner, one head per unit.  The result is bit-identical to the
+// happens in registers; otherwise the normalised head goes through LDS to
+// meet its partner.  Heads are read and written in place with streaming
+// loads and stores (the norm weights and the cos/sin rows, shared by every
+// head of a token, stay cached).  The result is bit-identical to the
 // reference.
 #include "v7g_device.h"
 #include "v7g_internal.h"
@@ -105,7 +106,9 @@ __device__ __forceinline__ void normalise(float4 (&xn)[K], const float4 (&x)[K],
   }
 }
 
-// head_dim % 64 == 0: HPU heads per 8-lane unit, rotation in registers.
+// head_dim % 64 == 0: HPU heads per 8-lane unit, rotation in registers.  One
+// head per unit measured fastest inside the per-layer chain (more heads per
+// unit raise the registers per thread and lower occupancy).
 template <int K, int HPU>
 __global__ __launch_bounds__(256) void rmsnorm_rope_reg_kernel(RopeArgs a) {
   constexpr int KH = K / 2;
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_reg_kernel(RopeArgs a) {
     hr[e] = head_ref(a, unit * HPU + e, m);
 #pragma unroll
     for (int k = 0; k < K; ++k)
-      x[e][k] = hr[e].live ? *reinterpret_cast<const float4 *>(hr[e].x + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      x[e][k] = hr[e].live ? ld_stream4(hr[e].x + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 #pragma unroll
   for (int e = 0; e < HPU; ++e) {
@@ -142,7 +145,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_reg_kernel(RopeArgs a) {
     }
     if (hr[e].live) {
 #pragma unroll
-      for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(hr[e].x + 32 * k) = xn[k];
+      for (int k = 0; k < K; ++k) st_stream4(hr[e].x + 32 * k, xn[k]);
     }
   }
 }
@@ -161,7 +164,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
   float4 x[K];
 #pragma unroll
   for (int k = 0; k < K; ++k)
-    x[k] = hr.live ? *reinterpret_cast<const float4 *>(hr.x + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    x[k] = hr.live ? ld_stream4(hr.x + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
   const float s = head_scale<K>(x, HD, a.eps);
   float4 xn[K];
   normalise<K>(xn, x, hr.w, s, hr.bad_pos);
@@ -192,14 +195,14 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
   }
   if (hr.live) {
 #pragma unroll
-    for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(hr.x + 32 * k) = xn[k];
+    for (int k = 0; k < K; ++k) st_stream4(hr.x + 32 * k, xn[k]);
   }
 }
 
 template <int K>
 static void launch_k(const RopeArgs &a, hipStream_t stream) {
   if ((32 * K) % 64 == 0) {
-    constexpr int HPU = 2;
+    constexpr int HPU = 1;
     const unsigned units = (a.n_heads + HPU - 1) / HPU;
     hipLaunchKernelGGL((rmsnorm_rope_reg_kernel<K, HPU>), dim3((units + 31u) / 32u), dim3(256), 0, stream, a);
   } else {

@@ -13,7 +13,7 @@
 // The reference group size is 64 (src/asm/v7_core.inc:120); GS is a template
 // parameter so 32-element blocks use the same algorithm.
 //
-// Vector layout: lane owns 4 consecutive floats (nontemporal dwordx4 loads of
+// Vector layout: lane owns 4 consecutive floats (streaming dwordx4 loads of
 // gate and up, or x), GS/4 consecutive lanes form one group, the group max is
 // a DPP butterfly inside 8 or 16 lanes, each lane stores its 4 codes as one
 // dword, and the first lane of the group stores the scale.  The divisions of
@@ -41,8 +41,8 @@ __global__ __launch_bounds__(kStreamBlock) void swiglu_f32_kernel(float *out, co
   for (long long c = (long long)blockIdx.x * kStreamBlock + threadIdx.x; c < n4; c += stride) {
     const float4 g = ld_stream4(gate + 4 * c);
     const float4 u = ld_stream4(up + 4 * c);
-    reinterpret_cast<float4 *>(out)[c] =
-        make_float4(swiglu_v7(g.x, u.x), swiglu_v7(g.y, u.y), swiglu_v7(g.z, u.z), swiglu_v7(g.w, u.w));
+    st_stream4(out + 4 * c,
+               make_float4(swiglu_v7(g.x, u.x), swiglu_v7(g.y, u.y), swiglu_v7(g.z, u.z), swiglu_v7(g.w, u.w)));
   }
 }
 
@@ -87,8 +87,8 @@ __global__ __launch_bounds__(kStreamBlock) void quantize_q8_flat_kernel(int8_t *
     m = (LPG == 8) ? group8_max(m) : group16_max(m);
     float scale, recip;
     q8_scale(m, scale, recip);
-    reinterpret_cast<uint32_t *>(out_q)[c] = pack4_codes(v, recip);
-    if ((threadIdx.x & (LPG - 1)) == 0) out_s[c / LPG] = scale;
+    st_stream_u32(reinterpret_cast<uint32_t *>(out_q) + c, pack4_codes(v, recip));
+    if ((threadIdx.x & (LPG - 1)) == 0) st_stream_f32(out_s + c / LPG, scale);
   }
 }
 
