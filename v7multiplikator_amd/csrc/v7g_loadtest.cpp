@@ -1,0 +1,441 @@
+// v7g_loadtest.cpp -- GPU leg of the reference's kernel load benchmarks
+// (tools/b_fused_add_rmsnorm_loadtest.cpp, b_rmsnorm_rope_loadtest.cpp,
+// b_swiglu_loadtest.cpp, b_swiglu_q8_loadtest.cpp): times one kernel of
+// libv7g.so on one GPU and prints the reference's "Pass: ... us / call (GB/s)"
+// lines, plus the fraction of MI355X's 8 TB/s HBM peak.
+//
+//   v7g_loadtest <libv7g.so> fused_add_rmsnorm <rows> <dim>
+//   v7g_loadtest <libv7g.so> rmsnorm_rope <tokens> <q_heads> <kv_heads> <head_dim>
+//   v7g_loadtest <libv7g.so> swiglu <rows> <hidden>
+//   v7g_loadtest <libv7g.so> swiglu_q8 <rows> <hidden> [gs]
+//   v7g_loadtest <libv7g.so> embedding <tokens> <vocab> <dim>
+//   v7g_loadtest <libv7g.so> configs          (every benchmark configuration below)
+//   options: --iterations N  --time secs  --no-rotate  --per-row
+//
+// Like the reference harnesses it loads the library with dlopen and resolves
+// each entry by name (src/v7_lib.h:585-739), warms up, optionally calibrates
+// the iteration count to --time, then times `iterations` calls.  Differences
+// that the GPU requires: buffers are device memory (hipMalloc) filled once
+// from a seeded host generator; time comes from HIP events on the library
+// stream; and, unless --no-rotate, the calls cycle through as many copies of
+// the buffers as it takes to exceed 512 MiB, so small shapes are not served
+// from the 256 MiB Infinity Cache (a cache-resident number is printed with
+// --no-rotate and labelled so).  --per-row calls the reference-signature
+// entry once per row, as the reference engine drives its kernels, to show
+// what a per-row launch costs on a GPU.  Bytes per call count every tensor
+// once (inputs read once, outputs written once).
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "v7g_lib.h"
+
+namespace {
+
+#define HIPCHECK(x)                                                                        \
+  do {                                                                                     \
+    hipError_t e_ = (x);                                                                   \
+    if (e_ != hipSuccess) {                                                                \
+      printf("Fail: HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, __LINE__); \
+      exit(1);                                                                             \
+    }                                                                                      \
+  } while (0)
+
+const double kPeakGBs = 8000.0;
+
+struct Lib {
+  void *h = nullptr;
+  int (*init)(void);
+  void (*set_stream)(void *);
+  int (*sync)(void);
+  int (*get_last_error)(void);
+  const char *(*error_string)(int);
+  int (*build_rope_tables)(float *, float *, int, int, float);
+  int (*fused_add_rmsnorm)(float *, float *, const float *, const float *, int, int, float);
+  int (*qk_rmsnorm_rope)(float *, long long, int, const float *, float *, long long, int, const float *, int, int,
+                         const float *, const float *, const int32_t *, int, int, int, float);
+  int (*swiglu_f32)(float *, const float *, const float *, long long);
+  int (*swiglu_q8)(int8_t *, float *, const float *, const float *, int, int, int);
+  int (*embedding_gather_q8)(float *, const int32_t *, int, const int8_t *, const float *, int, int);
+  v7s_fused_add_rmsnorm_fn v7s_fused_add_rmsnorm;
+  v7s_rmsnorm_rope_heads_fn v7s_rmsnorm_rope_heads;
+  v7s_swiglu_quantize_row_fn v7s_swiglu_quantize_row;
+  v7s_swiglu_row_fn v7s_swiglu_row;
+  v7s_embedding_row_fn v7s_embedding_row;
+};
+
+template <typename F>
+void resolve(Lib &L, F &fn, const char *name) {
+  void *p = dlsym(L.h, name);
+  if (!p) {
+    printf("[FATAL] missing symbol %s\n", name);
+    exit(1);
+  }
+  memcpy(&fn, &p, sizeof(p));
+}
+
+int load(const char *path, Lib &L) {
+  L.h = dlopen(path, RTLD_NOW | RTLD_LOCAL);
+  if (!L.h) {
+    printf("[v7g_loadtest] failed to load %s: %s\n", path, dlerror());
+    return -1;
+  }
+  resolve(L, L.init, "v7g_init");
+  resolve(L, L.set_stream, "v7g_set_stream");
+  resolve(L, L.sync, "v7g_sync");
+  resolve(L, L.get_last_error, "v7g_get_last_error");
+  resolve(L, L.error_string, "v7g_error_string");
+  resolve(L, L.build_rope_tables, "v7g_build_rope_tables");
+  resolve(L, L.fused_add_rmsnorm, "v7g_fused_add_rmsnorm");
+  resolve(L, L.qk_rmsnorm_rope, "v7g_qk_rmsnorm_rope");
+  resolve(L, L.swiglu_f32, "v7g_swiglu_f32");
+  resolve(L, L.swiglu_q8, "v7g_swiglu_q8");
+  resolve(L, L.embedding_gather_q8, "v7g_embedding_gather_q8");
+  resolve(L, L.v7s_fused_add_rmsnorm, "v7s_fused_add_rmsnorm");
+  resolve(L, L.v7s_rmsnorm_rope_heads, "v7s_rmsnorm_rope_heads");
+  resolve(L, L.v7s_swiglu_quantize_row, "v7s_swiglu_quantize_row");
+  resolve(L, L.v7s_swiglu_row, "v7s_swiglu_row");
+  resolve(L, L.v7s_embedding_row, "v7s_embedding_row");
+  return 0;
+}
+
+// splitmix64 -> uniform floats; the shapes, not the values, set the timing.
+struct Rng {
+  uint64_t s;
+  explicit Rng(uint64_t seed) : s(seed) {}
+  uint64_t next() {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+  float uniform(float lo, float hi) { return lo + (hi - lo) * (float)((next() >> 40) * (1.0 / 16777216.0)); }
+};
+
+template <typename T>
+T *device_fill(size_t n, Rng &r, float lo, float hi) {
+  std::vector<T> h(n);
+  for (size_t i = 0; i < n; ++i) h[i] = (T)r.uniform(lo, hi);
+  T *d = nullptr;
+  HIPCHECK(hipMalloc(&d, n * sizeof(T)));
+  HIPCHECK(hipMemcpy(d, h.data(), n * sizeof(T), hipMemcpyHostToDevice));
+  return d;
+}
+
+template <typename T>
+T *device_empty(size_t n) {
+  T *d = nullptr;
+  HIPCHECK(hipMalloc(&d, n * sizeof(T)));
+  return d;
+}
+
+struct Opts {
+  int iterations = 200;
+  double seconds = 0.0;
+  bool rotate = true;
+  bool per_row = false;
+};
+
+// Number of buffer sets so that one pass over them exceeds 512 MiB.
+int sets_for(double bytes_per_call, bool rotate) {
+  if (!rotate) return 1;
+  int n = (int)((512.0 * 1024 * 1024) / bytes_per_call) + 1;
+  return n < 1 ? 1 : (n > 64 ? 64 : n);
+}
+
+// Times `call(set)` with HIP events on `stream`: 3 warm-up rounds over every
+// set, optional calibration to opt.seconds, then the timed iterations.
+template <typename Call>
+double time_calls(const Lib &L, hipStream_t stream, int sets, const Opts &opt, Call call, int *iters_out) {
+  for (int w = 0; w < 3; ++w)
+    for (int s = 0; s < sets; ++s) call(s);
+  HIPCHECK(hipStreamSynchronize(stream));
+  hipEvent_t a, b;
+  HIPCHECK(hipEventCreate(&a));
+  HIPCHECK(hipEventCreate(&b));
+  int iters = opt.iterations;
+  if (opt.seconds > 0.0) {
+    HIPCHECK(hipEventRecord(a, stream));
+    for (int i = 0; i < 20; ++i) call(i % sets);
+    HIPCHECK(hipEventRecord(b, stream));
+    HIPCHECK(hipEventSynchronize(b));
+    float ms = 0.f;
+    HIPCHECK(hipEventElapsedTime(&ms, a, b));
+    iters = (int)(opt.seconds * 1e3 / (ms / 20.0) * 0.95);
+    if (iters < 10) iters = 10;
+  }
+  HIPCHECK(hipEventRecord(a, stream));
+  for (int i = 0; i < iters; ++i) call(i % sets);
+  HIPCHECK(hipEventRecord(b, stream));
+  HIPCHECK(hipEventSynchronize(b));
+  float ms = 0.f;
+  HIPCHECK(hipEventElapsedTime(&ms, a, b));
+  HIPCHECK(hipEventDestroy(a));
+  HIPCHECK(hipEventDestroy(b));
+  int err = L.get_last_error();
+  if (err) {
+    printf("Fail: library error %d (%s)\n", err, L.error_string(err));
+    exit(1);
+  }
+  *iters_out = iters;
+  return ms * 1e3 / iters;  // us per call
+}
+
+void report(const char *what, const std::string &shape, int iters, double us, double bytes, int sets) {
+  double gbs = bytes / (us * 1e-6) / 1e9;
+  const bool resident = bytes * sets < 512.0 * 1024 * 1024;  // the rotation fits the 256 MiB MALL twice over
+  printf("Pass: %s %s iterations=%d%s\n", what, shape.c_str(), iters,
+         resident ? "  (cache-resident: working set below 512 MiB)" : "");
+  printf("  %.3f us / call   (%.1f GB/s, %.1f%% of 8 TB/s)   bytes/call=%.0f buffer_sets=%d\n", us, gbs,
+         100.0 * gbs / kPeakGBs, bytes, sets);
+  printf("{\"kernel\": \"%s\", \"shape\": \"%s\", \"us\": %.3f, \"GBs\": %.1f, \"frac\": %.4f, \"bytes\": %.0f, "
+         "\"buffer_sets\": %d, \"iterations\": %d}\n",
+         what, shape.c_str(), us, gbs, gbs / kPeakGBs, bytes, sets, iters);
+  fflush(stdout);
+}
+
+void run_add_rmsnorm(const Lib &L, hipStream_t st, int rows, int dim, const Opts &opt) {
+  const size_t n = (size_t)rows * dim;
+  const double bytes = 4.0 * n * 4 + dim * 4.0;
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(1);
+  std::vector<float *> res(sets), add(sets), out(sets);
+  for (int s = 0; s < sets; ++s) {
+    res[s] = device_fill<float>(n, r, -1.f, 1.f);
+    add[s] = device_fill<float>(n, r, -1.f, 1.f);
+    out[s] = device_empty<float>(n);
+  }
+  float *w = device_fill<float>(dim, r, 0.5f, 1.5f);
+  int iters = 0;
+  double us;
+  char shape[96];
+  if (opt.per_row) {
+    us = time_calls(L, st, sets, opt, [&](int s) {
+      for (int i = 0; i < rows; ++i)
+        L.v7s_fused_add_rmsnorm(out[s] + (size_t)i * dim, res[s] + (size_t)i * dim, add[s] + (size_t)i * dim, w, dim);
+    }, &iters);
+    snprintf(shape, sizeof shape, "rows=%d dim=%d per-row-calls", rows, dim);
+  } else {
+    us = time_calls(L, st, sets, opt, [&](int s) { L.fused_add_rmsnorm(out[s], res[s], add[s], w, rows, dim, 1e-6f); },
+                    &iters);
+    snprintf(shape, sizeof shape, "rows=%d dim=%d", rows, dim);
+  }
+  report("fused_add_rmsnorm", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) {
+    HIPCHECK(hipFree(res[s]));
+    HIPCHECK(hipFree(add[s]));
+    HIPCHECK(hipFree(out[s]));
+  }
+  HIPCHECK(hipFree(w));
+}
+
+void run_rope(const Lib &L, hipStream_t st, int T, int nq, int nk, int hd, const Opts &opt) {
+  const long long ts = (long long)(nq + 2 * nk) * hd;  // fused QKV row: [Q | K | V]
+  const size_t n = (size_t)T * ts;
+  const double bytes = 2.0 * T * (nq + nk) * hd * 4 + 2.0 * T * (hd / 2) * 4 + 2.0 * hd * 4;
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(2);
+  std::vector<float *> qkv(sets);
+  for (int s = 0; s < sets; ++s) qkv[s] = device_fill<float>(n, r, -1.f, 1.f);
+  float *qw = device_fill<float>(hd, r, 0.5f, 1.5f), *kw = device_fill<float>(hd, r, 0.5f, 1.5f);
+  float *ct = device_empty<float>((size_t)T * hd / 2), *stb = device_empty<float>((size_t)T * hd / 2);
+  if (L.build_rope_tables(ct, stb, T, hd, 1e6f)) {
+    printf("Fail: rope tables\n");
+    exit(1);
+  }
+  std::vector<int32_t> hp(T);
+  for (int i = 0; i < T; ++i) hp[i] = i;
+  int32_t *pos = device_empty<int32_t>(T);
+  HIPCHECK(hipMemcpy(pos, hp.data(), T * 4, hipMemcpyHostToDevice));
+  int iters = 0;
+  double us;
+  char shape[128];
+  if (opt.per_row) {
+    us = time_calls(L, st, sets, opt, [&](int s) {
+      for (int t = 0; t < T; ++t) {
+        float *row = qkv[s] + (size_t)t * ts;
+        L.v7s_rmsnorm_rope_heads(row, nq, hd, qw, ct, stb, t, hd / 2);
+        L.v7s_rmsnorm_rope_heads(row + (size_t)nq * hd, nk, hd, kw, ct, stb, t, hd / 2);
+      }
+    }, &iters);
+    snprintf(shape, sizeof shape, "tokens=%d q_heads=%d kv_heads=%d head_dim=%d per-token-calls", T, nq, nk, hd);
+  } else {
+    us = time_calls(L, st, sets, opt, [&](int s) {
+      L.qk_rmsnorm_rope(qkv[s], ts, nq, qw, qkv[s] + (size_t)nq * hd, ts, nk, kw, T, hd, ct, stb, pos, 0, hd / 2, T,
+                        1e-6f);
+    }, &iters);
+    snprintf(shape, sizeof shape, "tokens=%d q_heads=%d kv_heads=%d head_dim=%d", T, nq, nk, hd);
+  }
+  report("rmsnorm_rope", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) HIPCHECK(hipFree(qkv[s]));
+  HIPCHECK(hipFree(qw));
+  HIPCHECK(hipFree(kw));
+  HIPCHECK(hipFree(ct));
+  HIPCHECK(hipFree(stb));
+  HIPCHECK(hipFree(pos));
+}
+
+void run_swiglu(const Lib &L, hipStream_t st, int rows, int hidden, int gs, bool q8, const Opts &opt) {
+  const size_t n = (size_t)rows * hidden;
+  const double bytes = q8 ? 2.0 * n * 4 + n + (double)rows * (hidden / gs) * 4 : 3.0 * n * 4;
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(3);
+  std::vector<float *> g(sets), u(sets), o(sets), sc(sets);
+  std::vector<int8_t *> q(sets);
+  for (int s = 0; s < sets; ++s) {
+    g[s] = device_fill<float>(n, r, -3.f, 3.f);
+    u[s] = device_fill<float>(n, r, -3.f, 3.f);
+    o[s] = q8 ? nullptr : device_empty<float>(n);
+    q[s] = q8 ? device_empty<int8_t>(n) : nullptr;
+    sc[s] = q8 ? device_empty<float>((size_t)rows * ((hidden + gs - 1) / gs)) : nullptr;
+  }
+  int iters = 0;
+  double us;
+  char shape[96];
+  if (opt.per_row) {
+    us = time_calls(L, st, sets, opt, [&](int s) {
+      for (int i = 0; i < rows; ++i) {
+        const size_t off = (size_t)i * hidden;
+        if (q8)
+          L.v7s_swiglu_quantize_row(reinterpret_cast<char *>(q[s] + off), g[s] + off, u[s] + off,
+                                    sc[s] + (size_t)i * ((hidden + 63) / 64), hidden);
+        else
+          L.v7s_swiglu_row(g[s] + off, u[s] + off, hidden);
+      }
+    }, &iters);
+    snprintf(shape, sizeof shape, "rows=%d hidden=%d%s per-row-calls", rows, hidden, q8 ? " gs=64" : "");
+  } else {
+    us = time_calls(L, st, sets, opt, [&](int s) {
+      if (q8)
+        L.swiglu_q8(q[s], sc[s], g[s], u[s], rows, hidden, gs);
+      else
+        L.swiglu_f32(o[s], g[s], u[s], (long long)n);
+    }, &iters);
+    if (q8)
+      snprintf(shape, sizeof shape, "rows=%d hidden=%d gs=%d", rows, hidden, gs);
+    else
+      snprintf(shape, sizeof shape, "rows=%d hidden=%d", rows, hidden);
+  }
+  report(q8 ? "swiglu_q8" : "swiglu_f32", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) {
+    HIPCHECK(hipFree(g[s]));
+    HIPCHECK(hipFree(u[s]));
+    if (o[s]) HIPCHECK(hipFree(o[s]));
+    if (q[s]) HIPCHECK(hipFree(q[s]));
+    if (sc[s]) HIPCHECK(hipFree(sc[s]));
+  }
+}
+
+void run_embedding(const Lib &L, hipStream_t st, int T, int vocab, int dim, const Opts &opt) {
+  const double bytes = (double)T * 4 + (double)T * dim + (double)T * (dim / 64) * 4 + (double)T * dim * 4;
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(4);
+  int8_t *tq = device_empty<int8_t>((size_t)vocab * dim);
+  {
+    std::vector<int8_t> h((size_t)vocab * dim);
+    for (auto &v : h) v = (int8_t)((int)(r.next() % 255u) - 127);
+    HIPCHECK(hipMemcpy(tq, h.data(), h.size(), hipMemcpyHostToDevice));
+  }
+  float *tsc = device_fill<float>((size_t)vocab * dim / 64, r, 0.001f, 0.02f);
+  std::vector<int32_t *> ids(sets);
+  std::vector<float *> out(sets);
+  std::vector<std::vector<int32_t>> hids(sets, std::vector<int32_t>(T));
+  for (int s = 0; s < sets; ++s) {
+    for (auto &v : hids[s]) v = (int32_t)(r.next() % (uint64_t)vocab);
+    ids[s] = device_empty<int32_t>(T);
+    HIPCHECK(hipMemcpy(ids[s], hids[s].data(), T * 4, hipMemcpyHostToDevice));
+    out[s] = device_empty<float>((size_t)T * dim);
+  }
+  v7g_q8_tensor desc{reinterpret_cast<char *>(tq), tsc};
+  int iters = 0;
+  double us;
+  char shape[96];
+  if (opt.per_row) {
+    us = time_calls(L, st, sets, opt, [&](int s) {
+      for (int t = 0; t < T; ++t) L.v7s_embedding_row(out[s] + (size_t)t * dim, hids[s][t], dim, &desc);
+    }, &iters);
+    snprintf(shape, sizeof shape, "tokens=%d vocab=%d dim=%d per-token-calls", T, vocab, dim);
+  } else {
+    us = time_calls(L, st, sets, opt, [&](int s) { L.embedding_gather_q8(out[s], ids[s], T, tq, tsc, dim, vocab); },
+                    &iters);
+    snprintf(shape, sizeof shape, "tokens=%d vocab=%d dim=%d", T, vocab, dim);
+  }
+  report("embedding_gather_q8", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) {
+    HIPCHECK(hipFree(ids[s]));
+    HIPCHECK(hipFree(out[s]));
+  }
+  HIPCHECK(hipFree(tq));
+  HIPCHECK(hipFree(tsc));
+}
+
+int usage() {
+  printf("usage: v7g_loadtest <libv7g.so> fused_add_rmsnorm <rows> <dim> | rmsnorm_rope <tokens> <q_heads> "
+         "<kv_heads> <head_dim> | swiglu <rows> <hidden> | swiglu_q8 <rows> <hidden> [gs] | embedding <tokens> "
+         "<vocab> <dim> | configs   [--iterations N] [--time secs] [--no-rotate] [--per-row]\n");
+  return 1;
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+  if (argc < 3) return usage();
+  Opts opt;
+  std::vector<std::string> pos;
+  for (int i = 2; i < argc; ++i) {
+    if (!strcmp(argv[i], "--iterations") && i + 1 < argc)
+      opt.iterations = atoi(argv[++i]);
+    else if (!strcmp(argv[i], "--time") && i + 1 < argc)
+      opt.seconds = atof(argv[++i]);
+    else if (!strcmp(argv[i], "--no-rotate"))
+      opt.rotate = false;
+    else if (!strcmp(argv[i], "--per-row"))
+      opt.per_row = true;
+    else
+      pos.push_back(argv[i]);
+  }
+  if (pos.empty() || opt.iterations < 1) return usage();
+  Lib L;
+  if (load(argv[1], L)) return 1;
+  if (L.init()) {
+    printf("Fail: v7g_init\n");
+    return 1;
+  }
+  hipStream_t st;
+  HIPCHECK(hipStreamCreate(&st));
+  L.set_stream(st);
+  auto num = [&](size_t i, int dflt) { return i < pos.size() ? atoi(pos[i].c_str()) : dflt; };
+  const std::string k = pos[0];
+  if (k == "fused_add_rmsnorm" && pos.size() >= 3)
+    run_add_rmsnorm(L, st, num(1, 0), num(2, 0), opt);
+  else if (k == "rmsnorm_rope" && pos.size() >= 5)
+    run_rope(L, st, num(1, 0), num(2, 0), num(3, 0), num(4, 0), opt);
+  else if (k == "swiglu" && pos.size() >= 3)
+    run_swiglu(L, st, num(1, 0), num(2, 0), 32, false, opt);
+  else if (k == "swiglu_q8" && pos.size() >= 3)
+    run_swiglu(L, st, num(1, 0), num(2, 0), num(3, 32), true, opt);
+  else if (k == "embedding" && pos.size() >= 4)
+    run_embedding(L, st, num(1, 0), num(2, 0), num(3, 0), opt);
+  else if (k == "configs") {
+    // The benchmark configurations: C1 .. C4, then the four kernels of the
+    // Qwen3-8B T=8192 per-layer chain (C5a .. C5d).
+    run_add_rmsnorm(L, st, 512, 2048, opt);
+    run_rope(L, st, 2048, 16, 8, 128, opt);
+    run_swiglu(L, st, 4096, 6144, 32, false, opt);
+    run_swiglu(L, st, 4096, 8192, 32, true, opt);
+    run_embedding(L, st, 8192, 151936, 4096, opt);
+    run_add_rmsnorm(L, st, 8192, 4096, opt);
+    run_rope(L, st, 8192, 32, 8, 128, opt);
+    run_swiglu(L, st, 8192, 12288, 32, true, opt);
+  } else {
+    return usage();
+  }
+  HIPCHECK(hipStreamDestroy(st));
+  return 0;
+}
