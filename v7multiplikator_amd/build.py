@@ -70,6 +70,20 @@ def build_loadtest(verbose: bool = False) -> str:
     return exe
 
 
+def build_test_shim(verbose: bool = False) -> str:
+    """Test support: tests/libdropin_shim.so, System V wrappers of the ms_abi drop-in entries."""
+    src = os.path.join(ROOT, "tests", "dropin_shim.c")
+    out = os.path.join(ROOT, "tests", "libdropin_shim.so")
+    cmd = ["gcc", "-O2", "-shared", "-fPIC", "-I", os.path.join(ROOT, "include"), "-o", out, src, "-L", PKG,
+           "-lv7g", "-Wl,-rpath,$ORIGIN/../v7multiplikator_amd"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"gcc failed ({res.returncode}):\n{res.stdout}{res.stderr}")
+    return out
+
+
 if __name__ == "__main__":
     print(build_library(verbose=True))
     if os.path.exists(os.path.join(CSRC, "v7g_loadtest.cpp")):
