@@ -65,6 +65,23 @@ typedef struct v7g_q8_tensor {
 typedef void(V7_ABI *v7s_fused_add_rmsnorm_fn)(float *o, float *residual, float *add, float *weight, int dim);
 V7_ABI void v7s_fused_add_rmsnorm(float *o, float *residual, float *add, float *weight, int dim);
 
+/* Replaces v7s_rmsnorm, typedef src/v7_lib.h:270, kernel src/asm/rmsnorm_kernel.inc:12-75:
+ * o = rmsnorm(x) * weight over one row.  Contract size % 32 == 0, size <= 16384. */
+typedef void(V7_ABI *v7s_rmsnorm_fn)(float *o, float *x, float *weight, int size);
+V7_ABI void v7s_rmsnorm(float *o, float *x, float *weight, int size);
+
+/* Replaces v7s_rmsnorm_quantize, typedef src/v7_lib.h:124, kernel
+ * src/asm/rmsnorm_quantize_kernel.inc:62-218: one row normalised and quantized
+ * per group of 64 (out_q[n] codes, out_s[n/64] scales), bit-identical to
+ * v7s_rmsnorm followed by v7d_quantize.  Contract n % 64 == 0, n <= 16384. */
+typedef void(V7_ABI *v7s_rmsnorm_quantize_fn)(char *out_q, float *in_x, float *out_s, int n, float *weight);
+V7_ABI void v7s_rmsnorm_quantize(char *out_q, float *in_x, float *out_s, int n, float *weight);
+
+/* Replaces v7s_add_inplace, typedef src/v7_lib.h:271, kernel src/asm/add_kernel.inc:26-49:
+ * x[i] += y[i] for n floats. */
+typedef void(V7_ABI *v7s_add_inplace_fn)(float *x, float *y, int n);
+V7_ABI void v7s_add_inplace(float *x, float *y, int n);
+
 /* Replaces v7s_rmsnorm_rope_heads, typedef src/v7_lib.h:273, dispatcher
  * src/asm/rmsnorm_rope_dispatch.inc:11-52.  n_heads heads of one token,
  * contiguous in buf, normalised and rotated in place at position pos; the
@@ -152,6 +169,26 @@ int v7g_arith_selfcheck(unsigned long long *mismatches);
  * pointers 16-byte aligned. */
 int v7g_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
                           float eps);
+
+/* rows x dim RMSNorm (v7s_rmsnorm per row): o = rmsnorm(x) * weight; o may
+ * alias x.  dim % 32 == 0, dim <= 16384, pointers 16-byte aligned. */
+int v7g_rmsnorm(float *o, const float *x, const float *weight, int rows, int dim, float eps);
+
+/* rows x dim RMSNorm -> Q8 (v7s_rmsnorm_quantize per row) with group size gs
+ * (32 or 64; the reference's is 64): out_q [rows*dim] int8, out_s [rows,
+ * dim/gs] f32.  dim % gs == 0, dim <= 16384. */
+int v7g_rmsnorm_quantize(int8_t *out_q, float *out_s, const float *x, const float *weight, int rows, int dim, int gs,
+                         float eps);
+
+/* The Q8 decode step v7s_add_inplace(residual, add) then v7s_rmsnorm_quantize
+ * (src/asm/forward_q8.inc:386-387) fused into one pass over rows x dim:
+ * residual += add (in place), then RMSNorm -> Q8 of the updated residual.
+ * No reference counterpart as one call; the results equal the two calls'. */
+int v7g_add_rmsnorm_quantize(int8_t *out_q, float *out_s, float *residual, const float *add, const float *weight,
+                             int rows, int dim, int gs, float eps);
+
+/* x[i] += y[i] for n floats (v7s_add_inplace); 16-byte aligned pointers. */
+int v7g_add_inplace(float *x, const float *y, long long n);
 
 /* RMSNorm+RoPE over n_tokens tokens of n_heads heads each.  Token t's heads
  * start at buf + t*token_stride (floats) and are contiguous.  Position of token

@@ -48,6 +48,9 @@ def lib():
             "orc_quantize_rows": (None, [_i8p, _f32p, _f32p, c_int, c_int, c_int]),
             "orc_swiglu_q8_rows": (None, [_i8p, _f32p, _f32p, _f32p, c_int, c_int, c_int]),
             "orc_embedding_gather": (None, [_f32p, _i32p, c_int, c_int, _i8p, _f32p]),
+            "orc_rmsnorm_rows": (None, [_f32p, _f32p, _f32p, c_int, c_int, c_float]),
+            "orc_rmsnorm_quantize_rows": (None, [_i8p, _f32p, _f32p, _f32p, c_int, c_int, c_int, c_float]),
+            "orc_add_inplace": (None, [_f32p, _f32p, c_ll]),
             "orc_avx2_available": (c_int, []),
             "orc_avx2_fused_add_rmsnorm": (None, [_f32p, _f32p, _f32p, _f32p, c_int, c_float]),
             "orc_avx2_rmsnorm_rope_heads": (None, [_f32p, c_int, c_int, _f32p, _f32p, _f32p, c_int, c_int, c_float]),
@@ -153,6 +156,34 @@ def embedding_gather(ids, table_q, table_s, dim):
     return out
 
 
+def rmsnorm(x, weight, eps):
+    """v7s_rmsnorm per row of x [rows, dim]."""
+    x = _c(x, np.float32)
+    dim = x.shape[-1]
+    o = np.empty_like(x)
+    lib().orc_rmsnorm_rows(o, x, _c(weight, np.float32), x.size // dim, dim, eps)
+    return o
+
+
+def rmsnorm_quantize(x, weight, eps, gs=64):
+    """v7s_rmsnorm_quantize per row: (codes like x, scales [rows, ceil(dim/gs)])."""
+    x = _c(x, np.float32)
+    dim = x.shape[-1]
+    rows = x.size // dim
+    spr = -(-dim // gs)
+    q = np.empty(x.size, np.int8)
+    s = np.empty(rows * spr, np.float32)
+    lib().orc_rmsnorm_quantize_rows(q, s, x.reshape(-1), _c(weight, np.float32), rows, dim, gs, eps)
+    return q.reshape(x.shape), s.reshape(rows, spr)
+
+
+def add_inplace(x, y):
+    """v7s_add_inplace: returns x + y (a copy of x updated)."""
+    x = _c(x, np.float32).copy()
+    lib().orc_add_inplace(x.reshape(-1), _c(y, np.float32).reshape(-1), x.size)
+    return x
+
+
 # --------------------------------------------------------------------------- AVX2 restatement (CPU baseline)
 
 def avx2_available():
@@ -233,6 +264,16 @@ def kt_quantize_c_ref(x):
         qi = np.rint(val).astype(np.int64)
         q[g * gs:g * gs + seg.size] = np.clip(qi, -127, 127).astype(np.int8)
     return q, s
+
+
+def kt_rmsnorm_c_ref(x, weight, eps):
+    """tools/kt_utils.h:450-458, float accumulation in element order, o = x*scale*w."""
+    x = _c(x, np.float32)
+    ss = np.float32(0)
+    for v in x:
+        ss = np.float32(ss + np.float32(v * v))
+    scale = np.float32(1.0) / np.sqrt(np.float32(ss / np.float32(x.size) + np.float32(eps)))
+    return ((x * scale).astype(np.float32) * _c(weight, np.float32)).astype(np.float32)
 
 
 def kt_fused_add_rmsnorm_c_ref(residual, add, weight, eps):

@@ -349,3 +349,52 @@ void orc_embedding_gather(float *out, const int32_t *ids, int n_tokens, int dim,
     for (int t = 0; t < n_tokens; ++t)
         orc_embedding_row(out + (long long)t * dim, ids[t], dim, table_q, table_s);
 }
+
+/* v7s_rmsnorm(o, x, weight, size): src/asm/rmsnorm_kernel.inc:12-75, typedef src/v7_lib.h:270.
+ * Contract size % 32 == 0 (no leftover blocks).  Phase 1 is the four-accumulator sum of squares
+ * (blocks 0,4,8.. into A, 1,5,.. into B, ...), (A+B)+(C+D), HADD_YMM; the scale is
+ * COMPUTE_RMS_SCALE with (float)size; phase 2 is o = (scale * x) * weight, two vmulps. */
+void orc_rmsnorm(float *o, const float *x, const float *weight, int size, float eps)
+{
+    float ss = orc_sumsq_lanes(x, size);
+    float s = orc_rms_scale(ss, size, eps);
+    for (int i = 0; i < size; ++i) {
+        float t = s * x[i];
+        o[i] = t * weight[i];
+    }
+}
+
+void orc_rmsnorm_rows(float *o, const float *x, const float *weight, int rows, int dim, float eps)
+{
+    for (int r = 0; r < rows; ++r)
+        orc_rmsnorm(o + (long long)r * dim, x + (long long)r * dim, weight, dim, eps);
+}
+
+/* v7s_rmsnorm_quantize(out_q, in_x, out_s, n, weight): src/asm/rmsnorm_quantize_kernel.inc:62-218,
+ * typedef src/v7_lib.h:124.  Phase 1 accumulates 64 floats per iteration, blocks 0..3 then 4..7 into
+ * A, B, C, D: the same block-to-accumulator assignment as v7s_rmsnorm for n % 64 == 0; the scale is
+ * vdivss by (float)n, + eps, vsqrtss, 1/x (:107-112).  Each 64-group of norm = (scale * x) * weight
+ * (:122-137) is quantized exactly as v7s_quantize_chunk does (:138-165).  The reference's validator
+ * requires the result to be bit-identical to the two-step chain v7s_rmsnorm -> v7d_quantize
+ * (tools/kt_utils.h:850-933), which is what this computes; gs is a parameter (the reference's is 64). */
+void orc_rmsnorm_quantize_rows(int8_t *out_q, float *out_s, const float *x, const float *weight, int rows, int dim,
+                               int gs, float eps)
+{
+    float *buf = (float *)malloc((size_t)dim * sizeof(float));
+    if (!buf)
+        return;
+    int spr = (dim + gs - 1) / gs;
+    for (int r = 0; r < rows; ++r) {
+        orc_rmsnorm(buf, x + (long long)r * dim, weight, dim, eps);
+        orc_quantize(out_q + (long long)r * dim, buf, out_s + (long long)r * spr, dim, gs);
+    }
+    free(buf);
+}
+
+/* v7s_add_inplace(x, y, n): src/asm/add_kernel.inc:26-49, typedef src/v7_lib.h:271.  x[i] = x[i] + y[i]
+ * (vaddps), n % 32 == 0. */
+void orc_add_inplace(float *x, const float *y, long long n)
+{
+    for (long long i = 0; i < n; ++i)
+        x[i] = x[i] + y[i];
+}

@@ -56,6 +56,14 @@ void orc_embedding_row(float *out, int token, int dim, const int8_t *table_q, co
 void orc_embedding_gather(float *out, const int32_t *ids, int n_tokens, int dim, const int8_t *table_q,
                           const float *table_s);
 
+/* next rows: v7s_rmsnorm (size % 32 == 0), v7s_rmsnorm_quantize (= quantize(rmsnorm), dim % gs == 0),
+ * v7s_add_inplace */
+void orc_rmsnorm(float *o, const float *x, const float *weight, int size, float eps);
+void orc_rmsnorm_rows(float *o, const float *x, const float *weight, int rows, int dim, float eps);
+void orc_rmsnorm_quantize_rows(int8_t *out_q, float *out_s, const float *x, const float *weight, int rows, int dim,
+                               int gs, float eps);
+void orc_add_inplace(float *x, const float *y, long long n);
+
 /* AVX2 restatement (v7_oracle_avx2.c): same results bit for bit, used as the CPU baseline */
 int orc_avx2_available(void);
 void orc_avx2_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int dim, float eps);

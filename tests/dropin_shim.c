@@ -43,3 +43,18 @@ void shim_rope_init(int head_dim, float rope_base)
 {
     v7s_rope_init(head_dim, rope_base);
 }
+
+void shim_rmsnorm(float *o, float *x, float *weight, int size)
+{
+    v7s_rmsnorm(o, x, weight, size);
+}
+
+void shim_rmsnorm_quantize(char *out_q, float *in_x, float *out_s, int n, float *weight)
+{
+    v7s_rmsnorm_quantize(out_q, in_x, out_s, n, weight);
+}
+
+void shim_add_inplace(float *x, float *y, int n)
+{
+    v7s_add_inplace(x, y, n);
+}

@@ -38,6 +38,9 @@ def shim():
     S.shim_swiglu_row.argtypes = [vp, vp, i]
     S.shim_swiglu_quantize_row.argtypes = [vp, vp, vp, vp, i]
     S.shim_rope_init.argtypes = [i, f]
+    S.shim_rmsnorm.argtypes = [vp, vp, vp, i]
+    S.shim_rmsnorm_quantize.argtypes = [vp, vp, vp, i, vp]
+    S.shim_add_inplace.argtypes = [vp, vp, i]
     torch.cuda.synchronize()
     L.v7g_set_stream(torch.cuda.current_stream().cuda_stream)
     L.v7g_clear_last_error()
@@ -161,3 +164,32 @@ def test_v7s_rope_init_tables(shim, oracle):
     wc, ws = oracle.rope_tables(4096, 128, 1e6)
     assert np.max(np.abs(tc.cpu().numpy() - wc.reshape(-1))) <= 1e-7
     assert np.max(np.abs(ts_.cpu().numpy() - ws.reshape(-1))) <= 1e-7
+
+
+@pytest.mark.parametrize("size", [64, 1024, 3072, 8192])
+def test_v7s_rmsnorm_and_rmsnorm_quantize(shim, oracle, size):
+    S, L = shim
+    L.v7g_set_rms_eps(1e-5)
+    x = C.validator_row(size, size)
+    w = C.validator_weight(size + 1, size)
+    xt, wt = dev(x), dev(w)
+    ot = torch.empty_like(xt)
+    S.shim_rmsnorm(ot.data_ptr(), xt.data_ptr(), wt.data_ptr(), size)
+    qt = torch.empty(size, dtype=torch.int8, device="cuda")
+    st = torch.empty(size // 64, dtype=torch.float32, device="cuda")
+    S.shim_rmsnorm_quantize(qt.data_ptr(), xt.data_ptr(), st.data_ptr(), size, wt.data_ptr())
+    done(L)
+    assert bits(ot.cpu().numpy(), oracle.rmsnorm(x[None], w, 1e-5)[0])
+    wq, ws = oracle.rmsnorm_quantize(x[None], w, 1e-5, 64)
+    assert bits(qt.cpu().numpy(), wq[0]) and bits(st.cpu().numpy(), ws[0])
+
+
+@pytest.mark.parametrize("n", [32, 96, 160, 2048, 2051])
+def test_v7s_add_inplace(shim, oracle, n):
+    S, L = shim
+    x = C.validator_row(n, n)
+    y = C.validator_row(n + 1, n)
+    xt, yt = dev(x), dev(y)
+    S.shim_add_inplace(xt.data_ptr(), yt.data_ptr(), n)
+    done(L)
+    assert bits(xt.cpu().numpy(), oracle.add_inplace(x, y))

@@ -316,3 +316,67 @@ def test_swiglu_q8_config4(ops, oracle):
     gq, gsc = ops.swiglu_q8(dev(g), dev(u), gs=32)
     assert_bits(host(gq), wq, "codes")
     assert_bits(host(gsc), ws, "scales")
+
+
+# --------------------------------------------------------------------------- rmsnorm, rmsnorm_quantize, add_inplace
+
+@pytest.mark.parametrize("dim", [64, 128, 256, 1024, 2048, 3072, 4096, 8192, 16384])
+@pytest.mark.parametrize("seed", [12345, 67890])
+def test_rmsnorm_rows(ops, oracle, dim, seed):
+    rows = 5
+    x = C.validator_row(seed, rows * dim).reshape(rows, dim)
+    w = C.validator_weight(seed + 1, dim)
+    for eps in (1e-6, 1e-5):
+        got = ops.rmsnorm(dev(x), dev(w), eps=eps)
+        assert_bits(host(got), oracle.rmsnorm(x, w, eps), f"rmsnorm dim={dim}")
+    xt = dev(x)
+    ops.rmsnorm(xt, dev(w), out=xt)  # in place
+    assert_bits(host(xt), oracle.rmsnorm(x, w, 1e-6), "rmsnorm in place")
+
+
+@pytest.mark.parametrize("gs", [64, 32])
+@pytest.mark.parametrize("dim", [64, 128, 512, 1024, 2048, 3072, 4096, 8192, 16384])
+def test_rmsnorm_quantize_rows(ops, oracle, gs, dim):
+    rows = 7
+    x = C.normal(dim + gs, (rows, dim))
+    w = C.norm_weight(dim, dim)
+    wq, ws = oracle.rmsnorm_quantize(x, w, 1e-6, gs)
+    q, s = ops.rmsnorm_quantize(dev(x), dev(w), eps=1e-6, gs=gs)
+    assert_bits(host(q), wq, "codes")
+    assert_bits(host(s), ws, "scales")
+
+
+@pytest.mark.parametrize("gs", [64, 32])
+@pytest.mark.parametrize("dim", [64, 2048, 4096])
+def test_add_rmsnorm_quantize_equals_the_two_calls(ops, oracle, gs, dim):
+    """The fused decode step equals v7s_add_inplace then v7s_rmsnorm_quantize (src/asm/forward_q8.inc:386-387)."""
+    rows = 9
+    r = C.normal(dim, (rows, dim))
+    a = C.normal(dim + 1, (rows, dim))
+    w = C.norm_weight(dim + 2, dim)
+    r_new = oracle.add_inplace(r, a)
+    wq, ws = oracle.rmsnorm_quantize(r_new, w, 1e-6, gs)
+    rt = dev(r)
+    q, s = ops.add_rmsnorm_quantize(rt, dev(a), dev(w), eps=1e-6, gs=gs)
+    assert_bits(host(rt), r_new, "residual")
+    assert_bits(host(q), wq, "codes")
+    assert_bits(host(s), ws, "scales")
+
+
+def test_rmsnorm_quantize_config_shape(ops, oracle):
+    """The Q8 path's per-token input to QKV/W1/W3 at the Qwen3-8B width: [2048, 4096], GS 64."""
+    x = C.normal(11, (2048, 4096))
+    w = C.norm_weight(12, 4096)
+    wq, ws = oracle.rmsnorm_quantize(x, w, 1e-6, 64)
+    q, s = ops.rmsnorm_quantize(dev(x), dev(w), eps=1e-6, gs=64)
+    assert_bits(host(q), wq, "codes")
+    assert_bits(host(s), ws, "scales")
+
+
+@pytest.mark.parametrize("n", [1, 3, 32, 96, 160, 1024, 2048, 100003])
+def test_add_inplace(ops, oracle, n):
+    x = C.normal(n, n)
+    y = C.normal(n + 1, n)
+    xt = dev(x)
+    ops.add_inplace(xt, dev(y))
+    assert_bits(host(xt), oracle.add_inplace(x, y), "add_inplace")

@@ -369,3 +369,61 @@ def test_avx2_matches_scalar_oracle(oracle):
     tq, ts = C.q8_table(9, 100, 512)
     ids = C.rng(10).integers(0, 100, 20).astype(np.int32)
     assert bits_equal(oracle.avx2_embedding_gather(ids, tq, ts, 512), oracle.embedding_gather(ids, tq, ts, 512))
+
+
+# --------------------------------------------------------------------------- next rows: rmsnorm, rmsnorm_quantize, add_inplace
+
+RMS_SIZES = [64, 128, 256, 1024, 2048, 3072, 8192]  # tools/v_rmsnorm_validate.cpp:51-61
+
+
+@pytest.mark.parametrize("size", RMS_SIZES)
+@pytest.mark.parametrize("seed", [12345, 67890])
+def test_rmsnorm_vs_validator_refs(oracle, size, seed):
+    """v7s_rmsnorm against the float C reference (tools/kt_utils.h:450-458) within 1e-3, the validator's
+    tolerance (tools/kt_utils.h:820), and against double precision within 1e-5 relative."""
+    x = C.validator_row(seed, size)
+    w = C.validator_weight(seed + 1, size)
+    o = oracle.rmsnorm(x[None], w, 1e-6)[0]
+    assert np.max(np.abs(o - oracle.kt_rmsnorm_c_ref(x, w, 1e-6))) < 1e-3
+    xd = x.astype(np.float64)
+    d = xd / np.sqrt(np.mean(xd * xd) + 1e-6) * w
+    assert np.max(np.abs(o - d) / np.maximum(np.abs(d), 1e-3)) < 1e-5
+
+
+def test_rmsnorm_order_matches_add_rmsnorm_and_known_answer(oracle):
+    """The two kernels accumulate in the same order for size % 32 == 0 (src/asm/rmsnorm_kernel.inc:22-48 and
+    add_rmsnorm_kernel.inc:29-73): with add = 0 the residual is unchanged and the outputs agree bit for bit.
+    Known answer: the accumulator-interleave input of the sum-of-squares test (sumsq 2^24 + 4) normalised with
+    w = 1 and eps = 0 scales by 1/sqrt((2^24 + 4)/64)."""
+    x = C.normal(77, (4, 1024))
+    w = C.norm_weight(78, 1024)
+    o, r = oracle.fused_add_rmsnorm(x, np.zeros_like(x), w, 1e-6)
+    assert bits_equal(r, x) and bits_equal(oracle.rmsnorm(x, w, 1e-6), o)
+    k = np.zeros(64, F)
+    k[0] = 4096.0
+    for i in (8, 16, 24, 32, 40):
+        k[i] = 1.0
+    s = F(1.0) / np.sqrt(F(F(TWO24 + 4) / F(64)))
+    assert bits_equal(oracle.rmsnorm(k[None], np.ones(64, F), 0.0)[0], (s * k).astype(F))
+
+
+@pytest.mark.parametrize("size", [64, 128, 256, 512, 1024, 2048, 3072, 8192])
+@pytest.mark.parametrize("seed", [12345, 67890])
+def test_rmsnorm_quantize_is_the_two_step_chain(oracle, size, seed):
+    """tools/kt_utils.h:850-933: v7s_rmsnorm_quantize must be bit-identical to v7s_rmsnorm -> v7d_quantize,
+    and close to the C-reference chain (non-FMA rounding may move a code by one)."""
+    x = C.validator_row(seed, size)
+    w = C.validator_weight(seed + 1, size)
+    q, s = oracle.rmsnorm_quantize(x[None], w, 1e-6, 64)
+    q2, s2 = oracle.quantize(oracle.rmsnorm(x[None], w, 1e-6), 64)
+    assert bits_equal(q, q2) and bits_equal(s, s2)
+    cq, _ = oracle.kt_quantize_c_ref(oracle.kt_rmsnorm_c_ref(x, w, 1e-6))
+    assert np.max(np.abs(q[0].astype(int) - cq.astype(int))) <= 1
+
+
+def test_add_inplace_exact(oracle):
+    """v7s_add_inplace: one binary32 add per element (tools/kt_utils.h:487-491, validator tolerance 1e-6)."""
+    for n in (32, 64, 96, 160, 2048):  # tools/v_add_inplace_validate.cpp:21
+        x = C.validator_row(n, n)
+        y = C.validator_row(n + 1, n)
+        assert bits_equal(oracle.add_inplace(x, y), (x + y).astype(F))

@@ -41,6 +41,10 @@ SIGNATURES = {
     "v7g_build_rope_tables": (_i, [_vp, _vp, _i, _i, _f]),
     "v7g_arith_selfcheck": (_i, [_vp]),
     "v7g_fused_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
+    "v7g_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f]),
+    "v7g_rmsnorm_quantize": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _f]),
+    "v7g_add_rmsnorm_quantize": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f]),
+    "v7g_add_inplace": (_i, [_vp, _vp, _ll]),
     "v7g_rmsnorm_rope_heads": (_i, [_vp, _i, _ll, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _f]),
     "v7g_qk_rmsnorm_rope": (_i, [_vp, _ll, _i, _vp, _vp, _ll, _i, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _i, _f]),
     "v7g_swiglu_f32": (_i, [_vp, _vp, _vp, _ll]),
@@ -52,6 +56,9 @@ SIGNATURES = {
 # ms_abi drop-in entries (reference names; not callable through ctypes on Linux).
 DROP_IN = [
     "v7s_fused_add_rmsnorm",
+    "v7s_rmsnorm",
+    "v7s_rmsnorm_quantize",
+    "v7s_add_inplace",
     "v7s_rmsnorm_rope_heads",
     "v7d_quantize",
     "v7s_embedding_row",

@@ -13,43 +13,52 @@
 // One workgroup per row: each thread keeps its float4 chunks of the row in
 // registers (4*(tid + k*TPR) for k < KMAX), so pass 1 issues every load of
 // residual and add together and pass 2 needs no second read; residual, add
-// and o move as streaming loads and stores, the weight row stays cached.  The updated
-// residual also goes to LDS, where 32 lanes of wave 0 replay the 32 FMA
-// chains (lane 8q + j is accumulator q, YMM lane j), conflict-free; the
+// and o move as streaming loads and stores, the weight row stays cached.  The
+// updated residual also goes to LDS, where 32 lanes of wave 0 replay the 32
+// FMA chains (lane 8q + j is accumulator q, YMM lane j), conflict-free; the
 // five-step xor exchange below is exactly the (A+B)+(C+D) + HADD_YMM pairing.
+//
+// The same row body serves the neighbours of this kernel in the reference:
+//   v7s_rmsnorm (src/asm/rmsnorm_kernel.inc:12-75): no add, same order;
+//   v7s_rmsnorm_quantize (src/asm/rmsnorm_quantize_kernel.inc:62-218): the
+//     normalised row quantized per group of 64 exactly as v7d_quantize does;
+//   and the Q8 decode step v7s_add_inplace -> v7s_rmsnorm_quantize
+//     (src/asm/forward_q8.inc:386-387), fused here into one pass.
 #include "v7g_device.h"
 #include "v7g_internal.h"
 
 namespace v7g {
 
-// o may alias residual (the row then ends as o, as in the reference); no
-// pointer is declared __restrict__.
-template <int TPR, int KMAX>
-__global__ __launch_bounds__(TPR) void fused_add_rmsnorm_kernel(float *o, float *residual, const float *add,
-                                                                const float *weight, int dim, float eps) {
+// One row.  ADD: the input is residual + add (residual updated in place),
+// else x.  QGS == 0: o = (s*x)*w; QGS = 32 or 64: the normalised row is
+// quantized in groups of QGS (codes q, scales q_s) and o is not written.
+// o may alias residual (the row then ends as o, as in the reference).
+template <int TPR, int KMAX, bool ADD, int QGS>
+__device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *xin, const float *add,
+                                        const float *weight, int dim, float eps) {
   extern __shared__ float row[];
   const int tid = threadIdx.x;
   const size_t r = blockIdx.x;
-  float *res = residual + r * (size_t)dim;
-  const float *ad = add + r * (size_t)dim;
-  float *out = o + r * (size_t)dim;
+  float *xr = xin + r * (size_t)dim;
 
-  // Pass 1: r = residual + add, written back and staged in LDS.
+  // Pass 1: load the row (and add), stage it in LDS.
   float4 x[KMAX], b[KMAX];
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int i = 4 * (tid + k * TPR);
     if (i < dim) {
-      x[k] = ld_stream4(res + i);
-      b[k] = ld_stream4(ad + i);
+      x[k] = ld_stream4(xr + i);
+      if constexpr (ADD) b[k] = ld_stream4(add + r * (size_t)dim + i);
     }
   }
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int i = 4 * (tid + k * TPR);
     if (i < dim) {
-      x[k] = make_float4(x[k].x + b[k].x, x[k].y + b[k].y, x[k].z + b[k].z, x[k].w + b[k].w);
-      st_stream4(res + i, x[k]);
+      if constexpr (ADD) {
+        x[k] = make_float4(x[k].x + b[k].x, x[k].y + b[k].y, x[k].z + b[k].z, x[k].w + b[k].w);
+        st_stream4(xr + i, x[k]);
+      }
       *reinterpret_cast<float4 *>(row + i) = x[k];
     }
   }
@@ -59,14 +68,14 @@ __global__ __launch_bounds__(TPR) void fused_add_rmsnorm_kernel(float *o, float 
     // The 32 FMA chains: lane v = 8q + j is YMM accumulator q (A..D), lane j.
     float acc = 0.0f;
     if (tid < 32) {
-      const int q = tid >> 3, j = tid & 7;
+      const int qa = tid >> 3, j = tid & 7;
       const int blocks = dim >> 3, left = blocks & 3, groups = blocks >> 2;
-      if (q == 0)
+      if (qa == 0)
         for (int bb = 0; bb < left; ++bb) {
           const float v = row[8 * bb + j];
           acc = __builtin_fmaf(v, v, acc);
         }
-      const float *p = row + 8 * (left + q) + j;
+      const float *p = row + 8 * (left + qa) + j;
 #pragma unroll 16
       for (int g = 0; g < groups; ++g) {
         const float v = p[32 * g];
@@ -86,40 +95,135 @@ __global__ __launch_bounds__(TPR) void fused_add_rmsnorm_kernel(float *o, float 
   __syncthreads();
   const float s = row[0];
 
-  // Pass 2: o = (s * r) * w.
+  // Pass 2: n = (s * x) * w, then either stored or quantized.
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int i = 4 * (tid + k * TPR);
-    if (i < dim) {
+    const bool live = i < dim;
+    float4 n = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) {
       const float4 w = *reinterpret_cast<const float4 *>(weight + i);
-      st_stream4(out + i, make_float4((s * x[k].x) * w.x, (s * x[k].y) * w.y, (s * x[k].z) * w.z, (s * x[k].w) * w.w));
+      n = make_float4((s * x[k].x) * w.x, (s * x[k].y) * w.y, (s * x[k].z) * w.z, (s * x[k].w) * w.w);
+    }
+    if constexpr (QGS == 0) {
+      if (live) st_stream4(o + r * (size_t)dim + i, n);
+    } else {
+      // QGS/4 consecutive lanes hold one group (dim % QGS == 0 and TPR % 16 == 0:
+      // a group is entirely live or entirely past the row); every lane takes
+      // part in the DPP butterfly.
+      constexpr int LPG = QGS / 4;
+      float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(n.x), __builtin_fabsf(n.y)),
+                                __builtin_fmaxf(__builtin_fabsf(n.z), __builtin_fabsf(n.w)));
+      m = (LPG == 8) ? group8_max(m) : group16_max(m);
+      float scale, recip;
+      q8_scale(m, scale, recip);
+      if (live) {
+        const size_t c = (r * (size_t)dim + i) >> 2;  // dword of 4 codes
+        st_stream_u32(reinterpret_cast<uint32_t *>(q) + c, pack4_codes(n, recip));
+        if ((tid & (LPG - 1)) == 0) st_stream_f32(q_s + r * (size_t)(dim / QGS) + (i / QGS), scale);
+      }
     }
   }
 }
 
 template <int TPR, int KMAX>
-static void launch_rows(float *o, float *residual, const float *add, const float *weight, int rows, int dim, float eps,
-                        hipStream_t stream) {
-  const size_t lds = (size_t)dim * sizeof(float);
-  hipLaunchKernelGGL((fused_add_rmsnorm_kernel<TPR, KMAX>), dim3(rows), dim3(TPR), lds, stream, o, residual, add,
-                     weight, dim, eps);
+__global__ __launch_bounds__(TPR) void fused_add_rmsnorm_kernel(float *o, float *residual, const float *add,
+                                                                const float *weight, int dim, float eps) {
+  rms_row<TPR, KMAX, true, 0>(o, nullptr, nullptr, residual, add, weight, dim, eps);
 }
+
+template <int TPR, int KMAX>
+__global__ __launch_bounds__(TPR) void rmsnorm_kernel(float *o, float *x, const float *weight, int dim, float eps) {
+  rms_row<TPR, KMAX, false, 0>(o, nullptr, nullptr, x, nullptr, weight, dim, eps);
+}
+
+template <int TPR, int KMAX, int QGS>
+__global__ __launch_bounds__(TPR) void rmsnorm_quantize_kernel(int8_t *q, float *q_s, float *x, const float *weight,
+                                                               int dim, float eps) {
+  rms_row<TPR, KMAX, false, QGS>(nullptr, q, q_s, x, nullptr, weight, dim, eps);
+}
+
+template <int TPR, int KMAX, int QGS>
+__global__ __launch_bounds__(TPR) void add_rmsnorm_quantize_kernel(int8_t *q, float *q_s, float *residual,
+                                                                   const float *add, const float *weight, int dim,
+                                                                   float eps) {
+  rms_row<TPR, KMAX, true, QGS>(nullptr, q, q_s, residual, add, weight, dim, eps);
+}
+
+// Chooses threads per row and float4 chunks per thread for dim <= 16384
+// (validated by the caller) and launches one workgroup per row.
+struct RowLaunch {
+  int rows, dim;
+  hipStream_t stream;
+  size_t lds() const { return (size_t)dim * sizeof(float); }
+};
+
+template <template <int, int> class Op, typename... A>
+static void dispatch_rows(const RowLaunch &L, A... args) {
+  if (L.dim <= 256)
+    Op<64, 1>::launch(L, args...);
+  else if (L.dim <= 1024)
+    Op<256, 1>::launch(L, args...);
+  else if (L.dim <= 2048)
+    Op<256, 2>::launch(L, args...);
+  else if (L.dim <= 4096)
+    Op<256, 4>::launch(L, args...);
+  else if (L.dim <= 8192)
+    Op<256, 8>::launch(L, args...);
+  else
+    Op<256, 16>::launch(L, args...);
+}
+
+template <int TPR, int KMAX>
+struct AddNormOp {
+  static void launch(const RowLaunch &L, float *o, float *residual, const float *add, const float *weight, float eps) {
+    hipLaunchKernelGGL((fused_add_rmsnorm_kernel<TPR, KMAX>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, o,
+                       residual, add, weight, L.dim, eps);
+  }
+};
+
+template <int TPR, int KMAX>
+struct NormOp {
+  static void launch(const RowLaunch &L, float *o, float *x, const float *weight, float eps) {
+    hipLaunchKernelGGL((rmsnorm_kernel<TPR, KMAX>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, o, x, weight, L.dim,
+                       eps);
+  }
+};
+
+template <int TPR, int KMAX>
+struct NormQ8Op {
+  static void launch(const RowLaunch &L, int8_t *q, float *q_s, float *x, const float *add, const float *weight,
+                     float eps, int gs) {
+    if (add) {
+      if (gs == 32)
+        hipLaunchKernelGGL((add_rmsnorm_quantize_kernel<TPR, KMAX, 32>), dim3(L.rows), dim3(TPR), L.lds(), L.stream,
+                           q, q_s, x, add, weight, L.dim, eps);
+      else
+        hipLaunchKernelGGL((add_rmsnorm_quantize_kernel<TPR, KMAX, 64>), dim3(L.rows), dim3(TPR), L.lds(), L.stream,
+                           q, q_s, x, add, weight, L.dim, eps);
+    } else {
+      if (gs == 32)
+        hipLaunchKernelGGL((rmsnorm_quantize_kernel<TPR, KMAX, 32>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, q,
+                           q_s, x, weight, L.dim, eps);
+      else
+        hipLaunchKernelGGL((rmsnorm_quantize_kernel<TPR, KMAX, 64>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, q,
+                           q_s, x, weight, L.dim, eps);
+    }
+  }
+};
 
 void launch_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
                               float eps, hipStream_t stream) {
-  // dim <= 16384 (validated by the caller): at most 16 float4 per thread.
-  if (dim <= 256)
-    launch_rows<64, 1>(o, residual, add, weight, rows, dim, eps, stream);
-  else if (dim <= 1024)
-    launch_rows<256, 1>(o, residual, add, weight, rows, dim, eps, stream);
-  else if (dim <= 2048)
-    launch_rows<256, 2>(o, residual, add, weight, rows, dim, eps, stream);
-  else if (dim <= 4096)
-    launch_rows<256, 4>(o, residual, add, weight, rows, dim, eps, stream);
-  else if (dim <= 8192)
-    launch_rows<256, 8>(o, residual, add, weight, rows, dim, eps, stream);
-  else
-    launch_rows<256, 16>(o, residual, add, weight, rows, dim, eps, stream);
+  dispatch_rows<AddNormOp>(RowLaunch{rows, dim, stream}, o, residual, add, weight, eps);
+}
+
+void launch_rmsnorm(float *o, const float *x, const float *weight, int rows, int dim, float eps, hipStream_t stream) {
+  dispatch_rows<NormOp>(RowLaunch{rows, dim, stream}, o, const_cast<float *>(x), weight, eps);
+}
+
+void launch_rmsnorm_quantize(int8_t *q, float *q_s, float *x, const float *add, const float *weight, int rows,
+                             int dim, int gs, float eps, hipStream_t stream) {
+  dispatch_rows<NormQ8Op>(RowLaunch{rows, dim, stream}, q, q_s, x, add, weight, eps, gs);
 }
 
 }  // namespace v7g

@@ -60,6 +60,29 @@ void launch_swiglu_f32(float *out, const float *gate, const float *up, long long
     hipLaunchKernelGGL(swiglu_f32_tail_kernel, dim3(1), dim3(4), 0, stream, out, gate, up, n4 * 4, n);
 }
 
+// v7s_add_inplace (src/asm/add_kernel.inc:26-49): x = x + y, one vaddps per
+// element; streamed like the kernels above.
+__global__ __launch_bounds__(kStreamBlock) void add_inplace_kernel(float *x, const float *y, long long n4) {
+  const long long stride = (long long)gridDim.x * kStreamBlock;
+  for (long long c = (long long)blockIdx.x * kStreamBlock + threadIdx.x; c < n4; c += stride) {
+    const float4 a = ld_stream4(x + 4 * c);
+    const float4 b = ld_stream4(y + 4 * c);
+    st_stream4(x + 4 * c, make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w));
+  }
+}
+
+__global__ void add_inplace_tail_kernel(float *x, const float *y, long long start, long long n) {
+  long long i = start + threadIdx.x;
+  if (i < n) x[i] = x[i] + y[i];
+}
+
+void launch_add_inplace(float *x, const float *y, long long n, hipStream_t stream) {
+  long long n4 = n / 4;
+  if (n4 > 0)
+    hipLaunchKernelGGL(add_inplace_kernel, dim3(stream_blocks(n4)), dim3(kStreamBlock), 0, stream, x, y, n4);
+  if (n % 4) hipLaunchKernelGGL(add_inplace_tail_kernel, dim3(1), dim3(4), 0, stream, x, y, n4 * 4, n);
+}
+
 // Flat path: every row length is a multiple of GS, so groups tile the flat
 // array and group g covers elements [g*GS, (g+1)*GS).  GS/4 consecutive lanes
 // hold one group (8 or 16 lanes, aligned inside the wave, so a group never

@@ -213,6 +213,53 @@ int v7g_fused_add_rmsnorm(float *o, float *residual, const float *add, const flo
   return check_launch();
 }
 
+int v7g_rmsnorm(float *o, const float *x, const float *weight, int rows, int dim, float eps) {
+  if (rows < 0 || dim <= 0 || dim % 32 != 0 || dim > kMaxNormDim) return fail(V7G_ERR_SHAPE);
+  if (rows == 0) return V7G_OK;
+  if (!o || !x || !weight) return fail(V7G_ERR_NULL);
+  if (!al16(o) || !al16(x) || !al16(weight)) return fail(V7G_ERR_ALIGN);
+  v7g::launch_rmsnorm(o, x, weight, rows, dim, eps, stream());
+  return check_launch();
+}
+
+static int check_norm_q8(const int8_t *out_q, const float *out_s, const float *x, const float *weight, int rows,
+                         int dim, int gs) {
+  if (rows < 0 || dim <= 0 || dim > kMaxNormDim || (gs != 32 && gs != 64) || dim % gs != 0) return V7G_ERR_SHAPE;
+  if (rows == 0) return V7G_OK;
+  if (!out_q || !out_s || !x || !weight) return V7G_ERR_NULL;
+  if (((uintptr_t)out_q & 3u) || ((uintptr_t)out_s & 3u) || !al16(x) || !al16(weight)) return V7G_ERR_ALIGN;
+  return V7G_OK;
+}
+
+int v7g_rmsnorm_quantize(int8_t *out_q, float *out_s, const float *x, const float *weight, int rows, int dim, int gs,
+                         float eps) {
+  int rc = check_norm_q8(out_q, out_s, x, weight, rows, dim, gs);
+  if (rc) return fail(rc);
+  if (rows == 0) return V7G_OK;
+  v7g::launch_rmsnorm_quantize(out_q, out_s, const_cast<float *>(x), nullptr, weight, rows, dim, gs, eps, stream());
+  return check_launch();
+}
+
+int v7g_add_rmsnorm_quantize(int8_t *out_q, float *out_s, float *residual, const float *add, const float *weight,
+                             int rows, int dim, int gs, float eps) {
+  int rc = check_norm_q8(out_q, out_s, residual, weight, rows, dim, gs);
+  if (!rc && rows > 0 && !add) rc = V7G_ERR_NULL;
+  if (!rc && rows > 0 && !al16(add)) rc = V7G_ERR_ALIGN;
+  if (rc) return fail(rc);
+  if (rows == 0) return V7G_OK;
+  v7g::launch_rmsnorm_quantize(out_q, out_s, residual, add, weight, rows, dim, gs, eps, stream());
+  return check_launch();
+}
+
+int v7g_add_inplace(float *x, const float *y, long long n) {
+  if (n < 0) return fail(V7G_ERR_SHAPE);
+  if (n == 0) return V7G_OK;
+  if (!x || !y) return fail(V7G_ERR_NULL);
+  if (!al16(x) || !al16(y)) return fail(V7G_ERR_ALIGN);
+  v7g::launch_add_inplace(x, y, n, stream());
+  return check_launch();
+}
+
 int v7g_rmsnorm_rope_heads(float *buf, int n_tokens, long long token_stride, int n_heads, int head_dim,
                            const float *norm_weight, const float *cos_table, const float *sin_table,
                            const int32_t *positions, int pos0, int rope_max_dim, int table_rows, float eps) {
@@ -298,6 +345,22 @@ int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const 
 
 V7_ABI void v7s_fused_add_rmsnorm(float *o, float *residual, float *add, float *weight, int dim) {
   v7g_fused_add_rmsnorm(o, residual, add, weight, 1, dim, g_eps.load());
+}
+
+V7_ABI void v7s_rmsnorm(float *o, float *x, float *weight, int size) {
+  v7g_rmsnorm(o, x, weight, 1, size, g_eps.load());
+}
+
+V7_ABI void v7s_rmsnorm_quantize(char *out_q, float *in_x, float *out_s, int n, float *weight) {
+  v7g_rmsnorm_quantize(reinterpret_cast<int8_t *>(out_q), out_s, in_x, weight, 1, n, 64, g_eps.load());
+}
+
+V7_ABI void v7s_add_inplace(float *x, float *y, int n) {
+  if (n < 0) {
+    fail(V7G_ERR_SHAPE);
+    return;
+  }
+  v7g_add_inplace(x, y, n);
 }
 
 V7_ABI void v7s_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, float *norm_weight, float *cos_table,

@@ -13,6 +13,17 @@ void launch_embedding_gather(float *out, const int32_t *ids, int n_tokens, const
 void launch_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
                               float eps, hipStream_t stream);
 
+// v7s_rmsnorm over rows x dim (dim % 32 == 0, <= 16384); o may alias x.
+void launch_rmsnorm(float *o, const float *x, const float *weight, int rows, int dim, float eps, hipStream_t stream);
+
+// RMSNorm -> Q8 over rows x dim (dim % gs == 0, gs 32 or 64); with add, x is a
+// residual updated in place as x + add first (add_inplace fused in front).
+void launch_rmsnorm_quantize(int8_t *q, float *q_s, float *x, const float *add, const float *weight, int rows,
+                             int dim, int gs, float eps, hipStream_t stream);
+
+// x += y over n floats (n % 4 == 0 on the vector path; any n).
+void launch_add_inplace(float *x, const float *y, long long n, hipStream_t stream);
+
 struct RopeSide {
   float *buf;               // first head of token 0
   long long token_stride;   // floats between consecutive tokens

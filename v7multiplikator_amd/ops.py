@@ -7,6 +7,10 @@ libv7g.so; nothing runs on the CPU and there is no fallback: without the built
 library the first call raises.
 
   fused_add_rmsnorm  <- v7s_fused_add_rmsnorm   (src/asm/add_rmsnorm_kernel.inc:15-129)
+  rmsnorm            <- v7s_rmsnorm             (src/asm/rmsnorm_kernel.inc:12-75)
+  rmsnorm_quantize   <- v7s_rmsnorm_quantize    (src/asm/rmsnorm_quantize_kernel.inc:62-218)
+  add_rmsnorm_quantize <- v7s_add_inplace then v7s_rmsnorm_quantize, one pass (src/asm/forward_q8.inc:386-387)
+  add_inplace        <- v7s_add_inplace         (src/asm/add_kernel.inc:26-49)
   rmsnorm_rope_heads <- v7s_rmsnorm_rope_heads  (src/asm/rmsnorm_rope_dispatch.inc:11-52)
   qk_rmsnorm_rope    <- v7s_qk_fork_heads, both sides in one launch (src/asm/qk_fork_kernel.inc:40-62)
   swiglu             <- .pq_ffn_silu            (src/asm/prefill_q8.inc:1159-1166)
@@ -58,6 +62,68 @@ def fused_add_rmsnorm(residual: torch.Tensor, add: torch.Tensor, weight: torch.T
                                            rows, dim, float(eps))
     _lib.check(rc, "fused_add_rmsnorm")
     return out
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = rmsnorm(x) * weight per row of x [rows, dim] (dim % 32 == 0); out may be x."""
+    _need(x, torch.float32, "x")
+    _need(weight, torch.float32, "weight")
+    dim = x.shape[-1]
+    if weight.numel() != dim:
+        raise ValueError("weight must be [dim]")
+    if out is None:
+        out = torch.empty_like(x)
+    _need(out, torch.float32, "out")
+    if out.shape != x.shape:
+        raise ValueError("out must match x")
+    _bind(x)
+    rc = _lib.load().v7g_rmsnorm(out.data_ptr(), x.data_ptr(), weight.data_ptr(), x.numel() // dim if dim else 0, dim,
+                                 float(eps))
+    _lib.check(rc, "rmsnorm")
+    return out
+
+
+def rmsnorm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6, gs: int = 64,
+                     out_q: torch.Tensor | None = None, out_s: torch.Tensor | None = None):
+    """RMSNorm then Q8 per row of x [rows, dim]: returns (codes int8 like x, scales [rows, dim/gs])."""
+    _need(x, torch.float32, "x")
+    _need(weight, torch.float32, "weight")
+    dim = x.shape[-1]
+    if weight.numel() != dim:
+        raise ValueError("weight must be [dim]")
+    rows, out_q, out_s = _q8_out(x.shape, dim, gs, x.device, out_q, out_s)
+    _bind(x)
+    rc = _lib.load().v7g_rmsnorm_quantize(out_q.data_ptr(), out_s.data_ptr(), x.data_ptr(), weight.data_ptr(), rows,
+                                          dim, int(gs), float(eps))
+    _lib.check(rc, "rmsnorm_quantize")
+    return out_q, out_s
+
+
+def add_rmsnorm_quantize(residual: torch.Tensor, add: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                         gs: int = 64, out_q: torch.Tensor | None = None, out_s: torch.Tensor | None = None):
+    """residual += add (in place), then RMSNorm -> Q8 of the updated rows: returns (codes, scales)."""
+    for t, n in ((residual, "residual"), (add, "add"), (weight, "weight")):
+        _need(t, torch.float32, n)
+    dim = residual.shape[-1]
+    if add.shape != residual.shape or weight.numel() != dim:
+        raise ValueError("shape mismatch: add must match residual, weight must be [dim]")
+    rows, out_q, out_s = _q8_out(residual.shape, dim, gs, residual.device, out_q, out_s)
+    _bind(residual)
+    rc = _lib.load().v7g_add_rmsnorm_quantize(out_q.data_ptr(), out_s.data_ptr(), residual.data_ptr(), add.data_ptr(),
+                                              weight.data_ptr(), rows, dim, int(gs), float(eps))
+    _lib.check(rc, "add_rmsnorm_quantize")
+    return out_q, out_s
+
+
+def add_inplace(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """x += y elementwise (v7s_add_inplace); returns x."""
+    _need(x, torch.float32, "x")
+    _need(y, torch.float32, "y")
+    if x.shape != y.shape:
+        raise ValueError("x and y must have the same shape")
+    _bind(x)
+    _lib.check(_lib.load().v7g_add_inplace(x.data_ptr(), y.data_ptr(), x.numel()), "add_inplace")
+    return x
 
 
 def _heads_view(buf: torch.Tensor, name: str):
