@@ -115,6 +115,14 @@ V7_ABI void v7s_swiglu_row(float *gate_inout, float *up, int hidden);
 typedef void(V7_ABI *v7s_swiglu_quantize_row_fn)(char *out_q, float *gate, float *up, float *out_s, int hidden);
 V7_ABI void v7s_swiglu_quantize_row(char *out_q, float *gate, float *up, float *out_s, int hidden);
 
+/* Replaces the engine-internal v7s_kv_pack_f16(dest, src, count),
+ * src/asm/kv_f16c.inc:12-52 (no export in src/v7_threading.def; exported
+ * here): dest[i] = binary16(src[i]), round to nearest even, for one K or V
+ * row of count floats.  Contract count > 0, count % 8 == 0; dest 8-byte and
+ * src 16-byte aligned. */
+typedef void(V7_ABI *v7s_kv_pack_f16_fn)(uint16_t *dest, float *src, int count);
+V7_ABI void v7s_kv_pack_f16(uint16_t *dest, float *src, int count);
+
 /* Replaces v7s_rope_init, typedef src/v7_lib.h:275, src/asm/fused_dispatch.inc:58-76:
  * builds the library-owned device cos/sin tables, [131072, head_dim/2] each
  * (positions 0..131071, src/asm/fused_f32_kernel.inc:9), freq_j =
@@ -151,13 +159,16 @@ int v7g_rope_init(int head_dim, float rope_base, int n_pos);
 int v7g_build_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base);
 
 /* Exhaustive self-check, on the current device, of the arithmetic identities
- * the kernels rely on to reproduce the reference's IEEE divisions with shorter
- * sequences: mismatches[0] = inputs d in [2^-126, 2^123) where rcp + one
- * Newton step differs from 1.0f/d; mismatches[1] = finite x >= 127*2^-126
- * where the fma-corrected x*(1/127) differs from x/127.0f; mismatches[2] =
- * non-NaN g where the sigmoid differs from EVAL_SIGMOID with vdivps
- * (src/asm/v7_macros.inc:98-160).  All three are 0 on a conforming device.
- * Synchronous; allocates a 96 KiB device buffer.  No reference counterpart. */
+ * the kernels rely on: mismatches[0] = inputs d in [2^-126, 2^123) where rcp
+ * + one Newton step differs from 1.0f/d; mismatches[1] = finite x >=
+ * 127*2^-126 where the fma-corrected x*(1/127) differs from x/127.0f;
+ * mismatches[2] = non-NaN g where the sigmoid differs from EVAL_SIGMOID with
+ * vdivps (src/asm/v7_macros.inc:98-160); mismatches[3] = binary32 patterns
+ * where the hardware binary16 conversion differs from round-to-nearest-even
+ * (the rounding of vcvtps2ph imm 0, src/asm/kv_f16c.inc), a NaN counting as
+ * correct when it gives a binary16 NaN.  mismatches must hold 4 values, all 0
+ * on a conforming device.  Synchronous; allocates a 128 KiB device buffer.
+ * No reference counterpart. */
 int v7g_arith_selfcheck(unsigned long long *mismatches);
 
 /* ---------------------------------------------------------------------------
@@ -206,6 +217,23 @@ int v7g_qk_rmsnorm_rope(float *q, long long q_token_stride, int n_q_heads, const
                         long long k_token_stride, int n_kv_heads, const float *k_norm_weight, int n_tokens,
                         int head_dim, const float *cos_table, const float *sin_table, const int32_t *positions,
                         int pos0, int rope_max_dim, int table_rows, float eps);
+
+/* v7g_qk_rmsnorm_rope that also writes the rotated K heads of token t as
+ * binary16 into k_cache + t*k_cache_stride (the v7s_kv_pack_f16 of the K row
+ * that follows RoPE, src/asm/forward_q8.inc:345-351, fused into the same
+ * pass).  keep_k_f32 = 0 skips writing the f32 K back in place.  k_cache
+ * 8-byte aligned, k_cache_stride % 4 == 0. */
+int v7g_qk_rmsnorm_rope_kv(float *q, long long q_token_stride, int n_q_heads, const float *q_norm_weight, float *k,
+                           long long k_token_stride, int n_kv_heads, const float *k_norm_weight, int n_tokens,
+                           int head_dim, const float *cos_table, const float *sin_table, const int32_t *positions,
+                           int pos0, int rope_max_dim, int table_rows, float eps, uint16_t *k_cache,
+                           long long k_cache_stride, int keep_k_f32);
+
+/* rows x row_len binary32 -> binary16 (v7s_kv_pack_f16 per row): row r from
+ * src + r*src_stride to dst + r*dst_stride (strides in elements).  row_len,
+ * strides % 4 == 0; dst 8-byte, src 16-byte aligned. */
+int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long long src_stride, int rows,
+                    int row_len);
 
 /* out[i] = (sigmoid(gate[i]) * gate[i]) * up[i] for n elements; out may alias gate. */
 int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n);

@@ -26,6 +26,7 @@ _lib = None
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 
 
 def lib():
@@ -51,6 +52,10 @@ def lib():
             "orc_rmsnorm_rows": (None, [_f32p, _f32p, _f32p, c_int, c_int, c_float]),
             "orc_rmsnorm_quantize_rows": (None, [_i8p, _f32p, _f32p, _f32p, c_int, c_int, c_int, c_float]),
             "orc_add_inplace": (None, [_f32p, _f32p, c_ll]),
+            "orc_kv_pack_f16": (None, [_u16p, _f32p, c_ll]),
+            "orc_avx2_kv_pack_f16": (None, [_u16p, _f32p, c_ll]),
+            "orc_f16c_available": (c_int, []),
+            "orc_check_f16_vs_f16c": (ctypes.c_ulonglong, [ctypes.c_uint64, ctypes.c_uint64, c_int]),
             "orc_avx2_available": (c_int, []),
             "orc_avx2_fused_add_rmsnorm": (None, [_f32p, _f32p, _f32p, _f32p, c_int, c_float]),
             "orc_avx2_rmsnorm_rope_heads": (None, [_f32p, c_int, c_int, _f32p, _f32p, _f32p, c_int, c_int, c_float]),
@@ -175,6 +180,29 @@ def rmsnorm_quantize(x, weight, eps, gs=64):
     s = np.empty(rows * spr, np.float32)
     lib().orc_rmsnorm_quantize_rows(q, s, x.reshape(-1), _c(weight, np.float32), rows, dim, gs, eps)
     return q.reshape(x.shape), s.reshape(rows, spr)
+
+
+def kv_pack_f16(x):
+    """v7s_kv_pack_f16: binary16 bit patterns (uint16, same shape) of x, round to nearest even."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_kv_pack_f16(out.reshape(-1), x.reshape(-1), x.size)
+    return out
+
+
+def f16c_available():
+    return bool(lib().orc_f16c_available())
+
+
+def avx2_kv_pack_f16(x):
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_avx2_kv_pack_f16(out.reshape(-1), x.reshape(-1), x.size)
+    return out
+
+
+def check_f16_vs_f16c(lo, count, threads):
+    return int(lib().orc_check_f16_vs_f16c(lo, count, threads))
 
 
 def add_inplace(x, y):

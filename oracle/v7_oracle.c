@@ -398,3 +398,47 @@ void orc_add_inplace(float *x, const float *y, long long n)
     for (long long i = 0; i < n; ++i)
         x[i] = x[i] + y[i];
 }
+
+/* binary32 -> binary16, round to nearest even, as vcvtps2ph with imm 0 does
+ * (src/asm/kv_f16c.inc:5-7: "nearest-even independently of MXCSR"):
+ * overflow to +-Inf, binary16 subnormals kept, NaN stays NaN with the top
+ * mantissa bits kept and the quiet bit set. */
+uint16_t orc_f32_to_f16_bits(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    uint32_t exp = (u >> 23) & 0xFFu;
+    uint32_t man = u & 0x7FFFFFu;
+    if (exp == 0xFFu) /* Inf or NaN */
+        return (uint16_t)(sign | 0x7C00u | (man ? (0x0200u | (man >> 13)) : 0u));
+    int e = (int)exp - 127 + 15; /* binary16 biased exponent */
+    if (e >= 31)
+        return (uint16_t)(sign | 0x7C00u); /* |f| >= 2^16: overflow (rounding cannot bring it back) */
+    if (e <= 0) {
+        /* binary16 subnormal or zero: value = m * 2^-24 with m = round(|f| * 2^24) */
+        if (e < -10)
+            return (uint16_t)sign; /* below half of the smallest subnormal (also f32 zeros/subnormals) */
+        uint32_t m = man | 0x800000u; /* implicit bit */
+        int shift = 14 - e;           /* 24-bit significand -> (11 + e - 1)-bit result */
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u)))
+            q += 1u; /* may carry into the smallest normal, which is the right encoding */
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u)))
+        q += 1u; /* a carry into the exponent is the correct result, up to Inf */
+    return (uint16_t)(sign | q);
+}
+
+/* v7s_kv_pack_f16(dest, src, count): src/asm/kv_f16c.inc:12-52 (internal in v7, called per token for the
+ * K and V rows after RoPE, src/asm/forward_q8.inc:345-358, prefill_q8.inc:157-171): dest[i] = f16(src[i]). */
+void orc_kv_pack_f16(uint16_t *dst, const float *src, long long n)
+{
+    for (long long i = 0; i < n; ++i)
+        dst[i] = orc_f32_to_f16_bits(src[i]);
+}

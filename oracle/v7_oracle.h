@@ -64,6 +64,14 @@ void orc_rmsnorm_quantize_rows(int8_t *out_q, float *out_s, const float *x, cons
                                int gs, float eps);
 void orc_add_inplace(float *x, const float *y, long long n);
 
+/* v7s_kv_pack_f16 (internal in v7): binary32 -> binary16 round-to-nearest-even */
+uint16_t orc_f32_to_f16_bits(float f);
+void orc_kv_pack_f16(uint16_t *dst, const float *src, long long n);
+/* the F16C instruction itself (vcvtps2ph imm 0) and an exhaustive comparison against orc_f32_to_f16_bits */
+int orc_f16c_available(void);
+void orc_avx2_kv_pack_f16(uint16_t *dst, const float *src, long long n);
+unsigned long long orc_check_f16_vs_f16c(uint64_t lo, uint64_t count, int n_threads);
+
 /* AVX2 restatement (v7_oracle_avx2.c): same results bit for bit, used as the CPU baseline */
 int orc_avx2_available(void);
 void orc_avx2_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int dim, float eps);

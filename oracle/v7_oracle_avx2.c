@@ -293,3 +293,75 @@ double orc_avx2_chain_bench(const orc_chain_args *a, int n_threads, int reps)
     clock_gettime(CLOCK_MONOTONIC, &ts1);
     return (double)(ts1.tv_sec - ts0.tv_sec) + 1e-9 * (double)(ts1.tv_nsec - ts0.tv_nsec);
 }
+
+/* kv_f16c.inc:12-52: vcvtps2ph with imm 0 (nearest-even), 8 floats at a time; n % 8 == 0. */
+__attribute__((target("avx2,f16c"))) void orc_avx2_kv_pack_f16(uint16_t *dst, const float *src, long long n)
+{
+    for (long long i = 0; i + 8 <= n; i += 8) {
+        __m128i h = _mm256_cvtps_ph(_mm256_loadu_ps(src + i), 0);
+        _mm_storeu_si128((__m128i *)(dst + i), h);
+    }
+}
+
+int orc_f16c_available(void)
+{
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("f16c");
+}
+
+/* Compares orc_f32_to_f16_bits with the F16C instruction (vcvtps2ph imm 0, the reference's instruction)
+ * for every binary32 bit pattern in [lo, lo + count), split over n_threads threads.  Returns the number
+ * of mismatches (NaN inputs included: both keep the top payload bits and set the quiet bit). */
+typedef struct {
+    uint64_t lo, hi;
+    unsigned long long bad;
+} f16_job;
+
+static __attribute__((target("avx2,f16c"))) void *f16_check_thread(void *p)
+{
+    f16_job *j = (f16_job *)p;
+    unsigned long long bad = 0;
+    uint32_t in[8];
+    uint16_t hw[8];
+    for (uint64_t b = j->lo; b < j->hi; b += 8) {
+        for (int k = 0; k < 8; ++k)
+            in[k] = (uint32_t)(b + (uint64_t)k < j->hi ? b + (uint64_t)k : j->hi - 1);
+        __m256 v = _mm256_loadu_ps((const float *)in);
+        _mm_storeu_si128((__m128i *)hw, _mm256_cvtps_ph(v, 0));
+        for (int k = 0; k < 8; ++k) {
+            float f;
+            memcpy(&f, &in[k], 4);
+            bad += orc_f32_to_f16_bits(f) != hw[k];
+        }
+    }
+    j->bad = bad;
+    return 0;
+}
+
+unsigned long long orc_check_f16_vs_f16c(uint64_t lo, uint64_t count, int n_threads)
+{
+    if (n_threads < 1)
+        n_threads = 1;
+    if (n_threads > 64)
+        n_threads = 64;
+    pthread_t th[64];
+    f16_job jobs[64];
+    uint64_t per = (count + (uint64_t)n_threads - 1) / (uint64_t)n_threads;
+    per = (per + 7) & ~(uint64_t)7;
+    for (int i = 0; i < n_threads; ++i) {
+        jobs[i].lo = lo + (uint64_t)i * per;
+        jobs[i].hi = jobs[i].lo + per;
+        if (jobs[i].hi > lo + count)
+            jobs[i].hi = lo + count;
+        if (jobs[i].lo > jobs[i].hi)
+            jobs[i].lo = jobs[i].hi;
+        jobs[i].bad = 0;
+        pthread_create(&th[i], 0, f16_check_thread, &jobs[i]);
+    }
+    unsigned long long total = 0;
+    for (int i = 0; i < n_threads; ++i) {
+        pthread_join(th[i], 0);
+        total += jobs[i].bad;
+    }
+    return total;
+}

@@ -58,3 +58,8 @@ void shim_add_inplace(float *x, float *y, int n)
 {
     v7s_add_inplace(x, y, n);
 }
+
+void shim_kv_pack_f16(uint16_t *dest, float *src, int count)
+{
+    v7s_kv_pack_f16(dest, src, count);
+}

@@ -41,6 +41,7 @@ def shim():
     S.shim_rmsnorm.argtypes = [vp, vp, vp, i]
     S.shim_rmsnorm_quantize.argtypes = [vp, vp, vp, i, vp]
     S.shim_add_inplace.argtypes = [vp, vp, i]
+    S.shim_kv_pack_f16.argtypes = [vp, vp, i]
     torch.cuda.synchronize()
     L.v7g_set_stream(torch.cuda.current_stream().cuda_stream)
     L.v7g_clear_last_error()
@@ -193,3 +194,14 @@ def test_v7s_add_inplace(shim, oracle, n):
     S.shim_add_inplace(xt.data_ptr(), yt.data_ptr(), n)
     done(L)
     assert bits(xt.cpu().numpy(), oracle.add_inplace(x, y))
+
+
+@pytest.mark.parametrize("count", [8, 24, 1024, 8 * 128])
+def test_v7s_kv_pack_f16_row(shim, oracle, count):
+    S, L = shim
+    x = C.normal(count, count, 4.0)
+    xt = dev(x)
+    ht = torch.empty(count, dtype=torch.float16, device="cuda")
+    S.shim_kv_pack_f16(ht.data_ptr(), xt.data_ptr(), count)
+    done(L)
+    assert bits(ht.cpu().numpy().view(np.uint16), oracle.kv_pack_f16(x))

@@ -57,15 +57,16 @@ def assert_bits(got, want, what=""):
 # --------------------------------------------------------------------------- arithmetic identities
 
 def test_arith_selfcheck_exhaustive(ops):
-    """rcp + Newton == 1/d, fma-corrected x/127 == IEEE x/127, and the sigmoid with both == EVAL_SIGMOID with
-    vdivps, each over its whole input range of binary32 patterns on this device."""
+    """rcp + Newton == 1/d, fma-corrected x/127 == IEEE x/127, the sigmoid with both == EVAL_SIGMOID with
+    vdivps, and the binary16 conversion == round-to-nearest-even, each over its whole input range of binary32
+    patterns on this device."""
     import ctypes
 
     from v7multiplikator_amd import _lib
-    counts = (ctypes.c_ulonglong * 3)()
+    counts = (ctypes.c_ulonglong * 4)()
     rc = _lib.load().v7g_arith_selfcheck(ctypes.addressof(counts))
     assert rc == 0
-    assert list(counts) == [0, 0, 0]
+    assert list(counts) == [0, 0, 0, 0]
 
 
 # --------------------------------------------------------------------------- embedding gather (a9)
@@ -380,3 +381,60 @@ def test_add_inplace(ops, oracle, n):
     xt = dev(x)
     ops.add_inplace(xt, dev(y))
     assert_bits(host(xt), oracle.add_inplace(x, y), "add_inplace")
+
+
+# --------------------------------------------------------------------------- v7s_kv_pack_f16, fused K pack
+
+F16_SPECIAL = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, -65520.0, 1e30, -1e30, 2.0 ** -24,
+                        2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -14 - 2.0 ** -25, 1e-30, np.inf, -np.inf, 0.1, 1 / 3.0,
+                        2049.0, 2051.0, 4097.5, -7.0e-6, 6.1e-5], np.float32)
+
+
+def test_kv_pack_f16_special_values(ops, oracle):
+    x = np.concatenate([F16_SPECIAL, np.zeros(8 - F16_SPECIAL.size % 8, np.float32)]).reshape(1, -1)
+    got = host(ops.kv_pack_f16(dev(x))).view(np.uint16)
+    assert_bits(got, oracle.kv_pack_f16(x), "special")
+    xn = np.full((1, 8), np.nan, np.float32)
+    gn = host(ops.kv_pack_f16(dev(xn))).view(np.uint16)
+    assert np.all((gn & 0x7C00) == 0x7C00) and np.all(gn & 0x03FF)
+
+
+@pytest.mark.parametrize("rows,row_len,src_stride,dst_stride", [(1, 8, 8, 8), (5, 1024, 1024, 1024),
+                                                                (37, 1024, 6144, 1024), (8192, 1024, 6144, 2048)])
+def test_kv_pack_f16_rows_strided(ops, oracle, rows, row_len, src_stride, dst_stride):
+    """K or V rows out of a fused QKV row [Q | K | V] into cache rows (strides in elements)."""
+    src = C.normal(rows + row_len, (rows, src_stride), 2.0)
+    st = dev(src)
+    cache = torch.zeros((rows, dst_stride), dtype=torch.float16, device="cuda")
+    ops.kv_pack_f16(st[:, :row_len], out=cache[:, :row_len])
+    got = host(cache).view(np.uint16)
+    assert_bits(got[:, :row_len], oracle.kv_pack_f16(src[:, :row_len]), "packed rows")
+    assert not got[:, row_len:].any()
+
+
+@pytest.mark.parametrize("keep", [True, False])
+@pytest.mark.parametrize("hd", [128, 96])
+def test_qk_rope_with_fused_k_pack(ops, oracle, keep, hd):
+    """RMSNorm+RoPE of Q and K plus the binary16 K cache rows in one launch == RoPE, then v7s_kv_pack_f16 of K."""
+    T, Hq, Hk = 67, 8, 2
+    qkv = C.normal(hd + 5, (T, (Hq + 2 * Hk) * hd))
+    qw = C.norm_weight(hd + 6, hd)
+    kw = C.norm_weight(hd + 7, hd)
+    ct, st = oracle.rope_tables(T + 3, hd, 1e6)
+    pos = (np.arange(T) + 3).astype(np.int32)
+    q_np = qkv[:, :Hq * hd].reshape(T, Hq, hd)
+    k_np = qkv[:, Hq * hd:(Hq + Hk) * hd].reshape(T, Hk, hd)
+    want_q = oracle.rmsnorm_rope(q_np, qw, ct, st, pos, 1e-6)
+    want_k = oracle.rmsnorm_rope(k_np, kw, ct, st, pos, 1e-6)
+    t = dev(qkv)
+    q = t[:, :Hq * hd].view(T, Hq, hd)
+    k = t[:, Hq * hd:(Hq + Hk) * hd].view(T, Hk, hd)
+    cache = torch.zeros((T + 4, Hk, hd), dtype=torch.float16, device="cuda")
+    ops.qk_rmsnorm_rope(q, k, dev(qw), dev(kw), dev(ct), dev(st), positions=dev(pos), eps=1e-6,
+                        k_cache=cache[2:2 + T], keep_k_f32=keep)
+    out = host(t)
+    assert_bits(out[:, :Hq * hd].reshape(T, Hq, hd), want_q, "q")
+    assert_bits(out[:, Hq * hd:(Hq + Hk) * hd].reshape(T, Hk, hd), want_k if keep else k_np, "k f32")
+    c = host(cache).view(np.uint16)
+    assert_bits(c[2:2 + T], oracle.kv_pack_f16(want_k), "k cache")
+    assert not c[:2].any() and not c[2 + T:].any()

@@ -427,3 +427,32 @@ def test_add_inplace_exact(oracle):
         x = C.validator_row(n, n)
         y = C.validator_row(n + 1, n)
         assert bits_equal(oracle.add_inplace(x, y), (x + y).astype(F))
+
+
+# --------------------------------------------------------------------------- v7s_kv_pack_f16
+
+f16c = pytest.mark.skipif("not __import__('oracle.oracle', fromlist=['x']).f16c_available()",
+                          reason="host CPU lacks F16C")
+
+
+@f16c
+def test_f16_conversion_exhaustive_vs_f16c(oracle):
+    """orc_f32_to_f16_bits equals vcvtps2ph with imm 0 -- the instruction src/asm/kv_f16c.inc uses -- for
+    every one of the 2^32 binary32 bit patterns, NaNs included."""
+    import os
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    assert oracle.check_f16_vs_f16c(0, 1 << 32, threads) == 0
+
+
+def test_kv_pack_f16_vs_numpy_and_f16c(oracle):
+    """numpy's float32 -> float16 cast is IEEE round-to-nearest-even: equal bit patterns on finite values,
+    overflow to Inf, binary16 subnormals and signed zeros."""
+    x = np.concatenate([C.normal(5, 4096, 3.0), C.normal(6, 1024, 3000.0), C.normal(7, 1024, 1e-5),
+                        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, -65520.0, 1e30, 2.0 ** -24, 2.0 ** -25,
+                                  3 * 2.0 ** -26, 2.0 ** -14 - 2.0 ** -25, np.inf, -np.inf], F)]).astype(F)
+    x = x[: (x.size // 8) * 8]
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert bits_equal(oracle.kv_pack_f16(x), want)
+    if oracle.f16c_available():
+        assert bits_equal(oracle.avx2_kv_pack_f16(x), want)

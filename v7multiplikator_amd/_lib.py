@@ -47,6 +47,9 @@ SIGNATURES = {
     "v7g_add_inplace": (_i, [_vp, _vp, _ll]),
     "v7g_rmsnorm_rope_heads": (_i, [_vp, _i, _ll, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _f]),
     "v7g_qk_rmsnorm_rope": (_i, [_vp, _ll, _i, _vp, _vp, _ll, _i, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _i, _f]),
+    "v7g_qk_rmsnorm_rope_kv": (_i, [_vp, _ll, _i, _vp, _vp, _ll, _i, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _i, _f,
+                                    _vp, _ll, _i]),
+    "v7g_kv_pack_f16": (_i, [_vp, _ll, _vp, _ll, _i, _i]),
     "v7g_swiglu_f32": (_i, [_vp, _vp, _vp, _ll]),
     "v7g_swiglu_q8": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "v7g_quantize_q8": (_i, [_vp, _vp, _vp, _i, _i, _i]),
@@ -65,6 +68,7 @@ DROP_IN = [
     "v7s_swiglu_row",
     "v7s_swiglu_quantize_row",
     "v7s_rope_init",
+    "v7s_kv_pack_f16",
 ]
 
 _lib = None

@@ -40,15 +40,20 @@ struct RopeArgs {
   int rope_max_dim;
   int table_rows;  // positions available in cos/sin; others give NaN rows
   float eps;
+  uint16_t *k_cache;         // optional: binary16 K rows (token t at k_cache + t*k_cache_stride)
+  long long k_cache_stride;  // binary16 elements between consecutive tokens
+  bool keep_k_f32;           // with k_cache: also write the f32 K heads back in place
 };
 
 // Where head f (flat over tokens x heads) lives, its weights and position.
 struct HeadRef {
   float *x;
   const float *w;
+  uint16_t *kc;  // binary16 cache address of this head's lane, K side with a cache only
   int pos;
   bool live;
   bool bad_pos;
+  bool write_f32;
 };
 
 __device__ __forceinline__ HeadRef head_ref(const RopeArgs &a, unsigned f, int m) {
@@ -61,6 +66,9 @@ __device__ __forceinline__ HeadRef head_ref(const RopeArgs &a, unsigned f, int m
   const int hs = h - (sd ? a.side[0].n_heads : 0);
   r.x = a.side[sd].buf + (size_t)t * (size_t)a.side[sd].token_stride + (size_t)hs * a.head_dim + 4 * m;
   r.w = a.side[sd].norm_weight + 4 * m;
+  const bool kpack = sd == 1 && a.k_cache != nullptr;
+  r.kc = kpack ? a.k_cache + (size_t)t * (size_t)a.k_cache_stride + (size_t)hs * a.head_dim + 4 * m : nullptr;
+  r.write_f32 = !kpack || a.keep_k_f32;
   int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
   // A position outside the tables cannot be read: its heads become NaN.
   r.bad_pos = pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
@@ -106,6 +114,20 @@ __device__ __forceinline__ void normalise(float4 (&xn)[K], const float4 (&x)[K],
   }
 }
 
+// The head's results: f32 in place, and/or binary16 into the K cache row
+// (v7s_kv_pack_f16 of the rotated K, src/asm/forward_q8.inc:345-351, fused).
+template <int K>
+__device__ __forceinline__ void store_head(const HeadRef &h, const float4 (&xn)[K]) {
+  if (h.write_f32) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) st_stream4(h.x + 32 * k, xn[k]);
+  }
+  if (h.kc) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) st_stream_u2(reinterpret_cast<uint32_t *>(h.kc + 32 * k), pack4_f16(xn[k]));
+  }
+}
+
 // head_dim % 64 == 0: HPU heads per 8-lane unit, rotation in registers.  One
 // head per unit measured fastest inside the per-layer chain (more heads per
 // unit raise the registers per thread and lower occupancy).
@@ -143,10 +165,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_reg_kernel(RopeArgs a) {
                                  __builtin_fmaf(od.z, c.z, ev.z * sn.z), __builtin_fmaf(od.w, c.w, ev.w * sn.w));
       }
     }
-    if (hr[e].live) {
-#pragma unroll
-      for (int k = 0; k < K; ++k) st_stream4(hr[e].x + 32 * k, xn[k]);
-    }
+    if (hr[e].live) store_head<K>(hr[e], xn);
   }
 }
 
@@ -193,10 +212,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
       xn[k] = make_float4(res[0], res[1], res[2], res[3]);
     }
   }
-  if (hr.live) {
-#pragma unroll
-    for (int k = 0; k < K; ++k) st_stream4(hr.x + 32 * k, xn[k]);
-  }
+  if (hr.live) store_head<K>(hr, xn);
 }
 
 template <int K>
@@ -212,7 +228,7 @@ static void launch_k(const RopeArgs &a, hipStream_t stream) {
 
 void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int head_dim, const float *cos_table,
                          const float *sin_table, const int32_t *positions, int pos0, int rope_max_dim, int table_rows,
-                         float eps, hipStream_t stream) {
+                         float eps, hipStream_t stream, uint16_t *k_cache, long long k_cache_stride, bool keep_k_f32) {
   RopeArgs a;
   a.n_sides = n_sides;
   a.side[0] = sides[0];
@@ -227,6 +243,9 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.rope_max_dim = rope_max_dim;
   a.table_rows = table_rows;
   a.eps = eps;
+  a.k_cache = n_sides > 1 ? k_cache : nullptr;
+  a.k_cache_stride = k_cache_stride;
+  a.keep_k_f32 = keep_k_f32;
   switch (head_dim / 32) {
     case 2: launch_k<2>(a, stream); break;
     case 3: launch_k<3>(a, stream); break;

@@ -4,9 +4,12 @@
 //   1. div127_rn(x) == x / 127.0f     for every finite x >= 127 * 2^-126
 //   2. sigmoid_v7(g) == the same sequence with max/min clamp and IEEE
 //      division (EVAL_SIGMOID as written, src/asm/v7_macros.inc:98-160) for
-//      every non-NaN binary32 g.
-// Each case walks its whole range of bit patterns (about 2^31, 2^31 and 2^32
-// values), a few milliseconds of GPU time.  Results are per-block counts in
+//      every non-NaN binary32 g;
+//   3. f16_bits(f) == a software binary32 -> binary16 round-to-nearest-even
+//      (the rounding of vcvtps2ph imm 0, src/asm/kv_f16c.inc) for every
+//      non-NaN binary32 f; a NaN must give a binary16 NaN.
+// Each case walks its whole range of bit patterns (about 2^31, 2^31, 2^32 and
+// 2^32 values), a few milliseconds of GPU time.  Results are per-block counts in
 // caller-visible device memory, summed on the host.
 #include <vector>
 
@@ -35,7 +38,32 @@ __device__ __forceinline__ float sigmoid_ieee(float g) {
   return 1.0f / (e + 1.0f);
 }
 
+// binary32 -> binary16, round to nearest even, in integer arithmetic.
+__device__ __forceinline__ uint32_t f16_bits_sw(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t exp = (u >> 23) & 0xFFu;
+  const uint32_t man = u & 0x7FFFFFu;
+  if (exp == 0xFFu) return sign | 0x7C00u | (man ? 0x0200u : 0u);
+  const int e = (int)exp - 112;  // binary16 biased exponent: exp - 127 + 15
+  if (e >= 31) return sign | 0x7C00u;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    const uint32_t m = man | 0x800000u;
+    const int shift = 14 - e;
+    uint32_t q = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q += 1u;
+    return sign | q;
+  }
+  uint32_t q = ((uint32_t)e << 10) | (man >> 13);
+  const uint32_t rem = man & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q += 1u;
+  return sign | q;
+}
+
 constexpr int kCheckBlocks = 4096;
+constexpr int kChecks = 4;
 
 __global__ __launch_bounds__(256) void arith_check_kernel(int which, uint64_t lo, uint64_t count,
                                                           unsigned long long *block_counts) {
@@ -51,10 +79,18 @@ __global__ __launch_bounds__(256) void arith_check_kernel(int which, uint64_t lo
     } else if (which == 1) {
       fast = div127_rn(v);
       exact = v / 127.0f;
-    } else {
+    } else if (which == 2) {
       if (v != v) continue;
       fast = sigmoid_v7(v);
       exact = sigmoid_ieee(v);
+    } else {
+      const uint32_t hw = f16_bits(v);
+      if (v != v) {
+        bad += (hw & 0x7C00u) != 0x7C00u || (hw & 0x03FFu) == 0u;  // must be a binary16 NaN
+        continue;
+      }
+      bad += hw != f16_bits_sw(v);
+      continue;
     }
     bad += __builtin_bit_cast(uint32_t, fast) != __builtin_bit_cast(uint32_t, exact);
   }
@@ -67,19 +103,20 @@ __global__ __launch_bounds__(256) void arith_check_kernel(int which, uint64_t lo
   if (threadIdx.x == 0) block_counts[blockIdx.x] = part[0];
 }
 
-int arith_selfcheck(unsigned long long mismatches[3], hipStream_t stream) {
+int arith_selfcheck(unsigned long long mismatches[4], hipStream_t stream) {
   struct Range {
     uint64_t lo, hi;
   };
-  const Range ranges[3] = {{0x00800000ull, 0x7D000000ull},    // [2^-126, 2^123)
-                           {0x03FE0000ull, 0x7F800000ull},    // [127*2^-126, Inf)
-                           {0x00000000ull, 0x100000000ull}};  // every pattern (NaNs skipped)
+  const Range ranges[kChecks] = {{0x00800000ull, 0x7D000000ull},    // [2^-126, 2^123)
+                                 {0x03FE0000ull, 0x7F800000ull},    // [127*2^-126, Inf)
+                                 {0x00000000ull, 0x100000000ull},   // every pattern (NaNs skipped)
+                                 {0x00000000ull, 0x100000000ull}};  // every pattern
   unsigned long long *d = nullptr;
-  if (hipMalloc(&d, sizeof(unsigned long long) * kCheckBlocks * 3) != hipSuccess) return -1;
-  for (int w = 0; w < 3; ++w)
+  if (hipMalloc(&d, sizeof(unsigned long long) * kCheckBlocks * kChecks) != hipSuccess) return -1;
+  for (int w = 0; w < kChecks; ++w)
     hipLaunchKernelGGL(arith_check_kernel, dim3(kCheckBlocks), dim3(256), 0, stream, w, ranges[w].lo,
                        ranges[w].hi - ranges[w].lo, d + (size_t)w * kCheckBlocks);
-  std::vector<unsigned long long> h((size_t)kCheckBlocks * 3);
+  std::vector<unsigned long long> h((size_t)kCheckBlocks * kChecks);
   int rc = 0;
   if (hipGetLastError() != hipSuccess ||
       hipMemcpyAsync(h.data(), d, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost, stream) !=
@@ -88,7 +125,7 @@ int arith_selfcheck(unsigned long long mismatches[3], hipStream_t stream) {
     rc = -1;
   (void)hipFree(d);
   if (rc) return rc;
-  for (int w = 0; w < 3; ++w) {
+  for (int w = 0; w < kChecks; ++w) {
     unsigned long long t = 0;
     for (int b = 0; b < kCheckBlocks; ++b) t += h[(size_t)w * kCheckBlocks + b];
     mismatches[w] = t;

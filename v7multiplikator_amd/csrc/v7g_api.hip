@@ -293,6 +293,42 @@ int v7g_qk_rmsnorm_rope(float *q, long long q_token_stride, int n_q_heads, const
   return check_launch();
 }
 
+int v7g_qk_rmsnorm_rope_kv(float *q, long long q_token_stride, int n_q_heads, const float *q_norm_weight, float *k,
+                           long long k_token_stride, int n_kv_heads, const float *k_norm_weight, int n_tokens,
+                           int head_dim, const float *cos_table, const float *sin_table, const int32_t *positions,
+                           int pos0, int rope_max_dim, int table_rows, float eps, uint16_t *k_cache,
+                           long long k_cache_stride, int keep_k_f32) {
+  int rc = check_rope_common(n_tokens, head_dim, cos_table, sin_table, rope_max_dim, table_rows);
+  if (!rc) rc = check_rope_side(q, q_token_stride, n_q_heads, head_dim, q_norm_weight, n_tokens);
+  if (!rc) rc = check_rope_side(k, k_token_stride, n_kv_heads, head_dim, k_norm_weight, n_tokens);
+  if (!rc) rc = check_rope_heads(n_tokens, n_q_heads + n_kv_heads);
+  if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
+  if (!rc && (k_cache_stride % 4 != 0 || (n_tokens > 1 && k_cache_stride < (long long)n_kv_heads * head_dim)))
+    rc = V7G_ERR_SHAPE;
+  if (!rc && n_tokens > 0 && !k_cache) rc = V7G_ERR_NULL;
+  if (!rc && ((uintptr_t)k_cache & 7u)) rc = V7G_ERR_ALIGN;
+  if (rc) return fail(rc);
+  if (n_tokens == 0) return V7G_OK;
+  v7g::RopeSide sides[2] = {{q, q_token_stride, n_q_heads, q_norm_weight},
+                            {k, k_token_stride, n_kv_heads, k_norm_weight}};
+  v7g::launch_rmsnorm_rope(sides, 2, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
+                           table_rows, eps, stream(), k_cache, k_cache_stride, keep_k_f32 != 0);
+  return check_launch();
+}
+
+int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long long src_stride, int rows,
+                    int row_len) {
+  if (rows < 0 || row_len <= 0 || row_len % 4 != 0 || dst_stride % 4 != 0 || src_stride % 4 != 0)
+    return fail(V7G_ERR_SHAPE);
+  if (rows > 1 && (dst_stride < row_len || src_stride < row_len)) return fail(V7G_ERR_SHAPE);
+  if ((long long)rows * (row_len / 4) >= (1LL << 32) - 256) return fail(V7G_ERR_SHAPE);
+  if (rows == 0) return V7G_OK;
+  if (!dst || !src) return fail(V7G_ERR_NULL);
+  if (((uintptr_t)dst & 7u) || !al16(src)) return fail(V7G_ERR_ALIGN);
+  v7g::launch_kv_pack_f16(dst, dst_stride, src, src_stride, rows, row_len, stream());
+  return check_launch();
+}
+
 int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n) {
   if (n < 0) return fail(V7G_ERR_SHAPE);
   if (n == 0) return V7G_OK;
@@ -345,6 +381,15 @@ int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const 
 
 V7_ABI void v7s_fused_add_rmsnorm(float *o, float *residual, float *add, float *weight, int dim) {
   v7g_fused_add_rmsnorm(o, residual, add, weight, 1, dim, g_eps.load());
+}
+
+V7_ABI void v7s_kv_pack_f16(uint16_t *dest, float *src, int count) {
+  // The reference's contract: count is a positive multiple of 8 (src/asm/kv_f16c.inc:6).
+  if (count <= 0 || count % 8 != 0) {
+    fail(V7G_ERR_SHAPE);
+    return;
+  }
+  v7g_kv_pack_f16(dest, count, src, count, 1, count);
 }
 
 V7_ABI void v7s_rmsnorm(float *o, float *x, float *weight, int size) {

@@ -105,6 +105,19 @@ __device__ __forceinline__ uint32_t pack4_codes(float4 v, float recip) {
          (q8_code_byte(v.w * recip) << 24);
 }
 
+// binary32 -> binary16 with round to nearest even (v_cvt_f16_f32 in the
+// default rounding mode, binary16 subnormals kept), the conversion of the
+// reference's vcvtps2ph with imm 0 (src/asm/kv_f16c.inc:5-7); finite inputs
+// and infinities give identical bits, NaN stays NaN.  v7g_arith_selfcheck()
+// compares it with a software rounding over every binary32 pattern.
+__device__ __forceinline__ uint32_t f16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+// Four floats as four binary16 values in two dwords (little-endian order).
+__device__ __forceinline__ uint2 pack4_f16(float4 v) {
+  return make_uint2(f16_bits(v.x) | (f16_bits(v.y) << 16), f16_bits(v.z) | (f16_bits(v.w) << 16));
+}
+
 // Streaming (nontemporal) loads and stores for activations that each kernel
 // reads or writes exactly once.  They keep the stream out of L2 and the
 // Infinity Cache (MALL): the reused lines (RoPE tables, norm weights, table
@@ -123,6 +136,11 @@ __device__ __forceinline__ void st_stream4(float *p, float4 v) {
 __device__ __forceinline__ uint32_t ld_stream_u32(const uint32_t *p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_stream_u32(uint32_t *p, uint32_t v) { __builtin_nontemporal_store(v, p); }
 __device__ __forceinline__ void st_stream_f32(float *p, float v) { __builtin_nontemporal_store(v, p); }
+typedef unsigned int v7g_u2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void st_stream_u2(uint32_t *p, uint2 v) {
+  v7g_u2 a = {v.x, v.y};
+  __builtin_nontemporal_store(a, reinterpret_cast<v7g_u2 *>(p));
+}
 
 // DPP lane exchanges inside a 16-lane row (gfx9 encodings).
 enum : int {

@@ -30,9 +30,17 @@ struct RopeSide {
   int n_heads;
   const float *norm_weight; // [head_dim]
 };
+// With two sides (Q, K) and k_cache != nullptr, the rotated K heads are also
+// written as binary16 rows of the KV cache (and in place as f32 only if
+// keep_k_f32).
 void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int head_dim, const float *cos_table,
                          const float *sin_table, const int32_t *positions, int pos0, int rope_max_dim, int table_rows,
-                         float eps, hipStream_t stream);
+                         float eps, hipStream_t stream, uint16_t *k_cache = nullptr, long long k_cache_stride = 0,
+                         bool keep_k_f32 = true);
+
+// binary32 -> binary16 rows (v7s_kv_pack_f16): rows x row_len (row_len % 4 == 0).
+void launch_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long long src_stride, int rows,
+                        int row_len, hipStream_t stream);
 
 void launch_swiglu_f32(float *out, const float *gate, const float *up, long long n, hipStream_t stream);
 
@@ -42,10 +50,11 @@ void launch_swiglu_f32(float *out, const float *gate, const float *up, long long
 void launch_quantize_q8(int8_t *out_q, float *out_s, const float *x, const float *gate, const float *up, int rows,
                         int row_len, int gs, hipStream_t stream);
 
-// Exhaustive check of rcp_rn, div127_rn and sigmoid_v7 against IEEE division
-// on the current device (synchronous; allocates a small device buffer).
+// Exhaustive check of rcp_rn, div127_rn and sigmoid_v7 against IEEE division,
+// and of f16_bits against a software rounding, on the current device
+// (synchronous; allocates a small device buffer).
 // mismatches[i] = number of inputs where identity i fails; returns 0 or -1 on
 // a HIP error.
-int arith_selfcheck(unsigned long long mismatches[3], hipStream_t stream);
+int arith_selfcheck(unsigned long long mismatches[4], hipStream_t stream);
 
 }  // namespace v7g

@@ -18,6 +18,7 @@ library the first call raises.
   swiglu_q8          <- SwiGLU then v7d_quantize (src/asm/prefill_q8.inc:1154-1183)
   embedding_gather_q8 <- v7s_embedding_row      (src/asm/forward.inc:13-42)
   rope_tables        <- v7s_rope_init           (src/asm/fused_dispatch.inc:58-76)
+  kv_pack_f16        <- v7s_kv_pack_f16         (src/asm/kv_f16c.inc:12-52)
 """
 from __future__ import annotations
 
@@ -164,8 +165,13 @@ def rmsnorm_rope_heads(buf: torch.Tensor, norm_weight: torch.Tensor, cos_table: 
 
 def qk_rmsnorm_rope(q: torch.Tensor, k: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
                     cos_table: torch.Tensor, sin_table: torch.Tensor, positions: torch.Tensor | None = None,
-                    pos0: int = 0, eps: float = 1e-6) -> None:
-    """In-place RMSNorm+RoPE of Q [T, Hq, D] and K [T, Hk, D] in one launch."""
+                    pos0: int = 0, eps: float = 1e-6, k_cache: torch.Tensor | None = None,
+                    keep_k_f32: bool = True) -> None:
+    """In-place RMSNorm+RoPE of Q [T, Hq, D] and K [T, Hk, D] in one launch.
+
+    With k_cache (float16 [T, Hk, D], heads of a token contiguous, token stride free), the rotated K heads
+    are also written there as binary16 (v7s_kv_pack_f16 fused); keep_k_f32=False leaves K's f32 storage
+    untouched."""
     for t, n in ((q, "q"), (k, "k")):
         _need(t, torch.float32, n, contiguous=False)
     for t, n in ((q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight"), (cos_table, "cos_table"),
@@ -176,11 +182,23 @@ def qk_rmsnorm_rope(q: torch.Tensor, k: torch.Tensor, q_norm_weight: torch.Tenso
     if Tk != T or Dk != D:
         raise ValueError("q and k must have the same tokens and head_dim")
     _bind(q)
-    rc = _lib.load().v7g_qk_rmsnorm_rope(q.data_ptr(), qs, Hq, q_norm_weight.data_ptr(), k.data_ptr(), ks, Hk,
-                                         k_norm_weight.data_ptr(), T, D, cos_table.data_ptr(), sin_table.data_ptr(),
-                                         _positions(positions, T, q.device), int(pos0), cos_table.shape[-1],
-                                         cos_table.shape[0], float(eps))
-    _lib.check(rc, "qk_rmsnorm_rope")
+    if k_cache is None:
+        rc = _lib.load().v7g_qk_rmsnorm_rope(q.data_ptr(), qs, Hq, q_norm_weight.data_ptr(), k.data_ptr(), ks, Hk,
+                                             k_norm_weight.data_ptr(), T, D, cos_table.data_ptr(),
+                                             sin_table.data_ptr(), _positions(positions, T, q.device), int(pos0),
+                                             cos_table.shape[-1], cos_table.shape[0], float(eps))
+        _lib.check(rc, "qk_rmsnorm_rope")
+        return
+    _need(k_cache, torch.float16, "k_cache", contiguous=False)
+    Tc, Hc, Dc, cs = _heads_view(k_cache, "k_cache")
+    if (Tc, Hc, Dc) != (T, Hk, D):
+        raise ValueError("k_cache must be [tokens, kv_heads, head_dim]")
+    rc = _lib.load().v7g_qk_rmsnorm_rope_kv(q.data_ptr(), qs, Hq, q_norm_weight.data_ptr(), k.data_ptr(), ks, Hk,
+                                            k_norm_weight.data_ptr(), T, D, cos_table.data_ptr(),
+                                            sin_table.data_ptr(), _positions(positions, T, q.device), int(pos0),
+                                            cos_table.shape[-1], cos_table.shape[0], float(eps),
+                                            k_cache.data_ptr(), cs, int(bool(keep_k_f32)))
+    _lib.check(rc, "qk_rmsnorm_rope_kv")
 
 
 def swiglu(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -261,6 +279,23 @@ def embedding_gather_q8(ids: torch.Tensor, table_q: torch.Tensor, table_s: torch
     rc = _lib.load().v7g_embedding_gather_q8(out.data_ptr(), ids.data_ptr(), n, table_q.data_ptr(),
                                              table_s.data_ptr(), dim, vocab)
     _lib.check(rc, "embedding_gather_q8")
+    return out
+
+
+def kv_pack_f16(src: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """binary16 copy (round to nearest even) of src [rows, row_len] f32; row strides free (row_len % 4 == 0)."""
+    _need(src, torch.float32, "src", contiguous=False)
+    if src.dim() != 2 or src.stride(1) != 1:
+        raise ValueError("src must be [rows, row_len] with contiguous rows")
+    rows, n = src.shape
+    if out is None:
+        out = torch.empty((rows, n), dtype=torch.float16, device=src.device)
+    _need(out, torch.float16, "out", contiguous=False)
+    if out.shape != src.shape or out.stride(1) != 1:
+        raise ValueError("out must be [rows, row_len] with contiguous rows")
+    _bind(src)
+    rc = _lib.load().v7g_kv_pack_f16(out.data_ptr(), out.stride(0), src.data_ptr(), src.stride(0), rows, n)
+    _lib.check(rc, "kv_pack_f16")
     return out
 
 
