@@ -194,12 +194,15 @@ def cpu_baseline(torch, ops, chain, args):
                  and np.array_equal(qkv_g[:, :NQ * HD], q_h) and np.array_equal(qkv_g[:, NQ * HD:(NQ + NKV) * HD], k_h)
                  and np.array_equal(hostc(sub.codes), codes_c) and np.array_equal(hostc(sub.scales), scales_c))
 
-    # Timing: a warm repetition, a 3-repetition calibration, then about cpu_seconds of work.
+    # Timing: a warm repetition, then rounds of repetitions until cpu_seconds of work have been timed.
     r_t, q_t, k_t = residual0.copy(), q_h.copy(), k_h.copy()
     run(1, cores, r_t, q_t, k_t)
-    t3, *_ = run(3, cores, r_t, q_t, k_t)
-    reps = max(3, int(args.cpu_seconds / max(t3 / 3, 1e-6)))
-    secs, *_ = run(reps, cores, r_t, q_t, k_t)
+    secs, reps, chunk = 0.0, 0, 2
+    while secs < args.cpu_seconds:
+        t, *_ = run(chunk, cores, r_t, q_t, k_t)
+        secs += t
+        reps += chunk
+        chunk = max(2, int(chunk * min(4.0, max(1.2, (args.cpu_seconds - secs) / max(t, 1e-6) * 0.5))))
     chain_bytes = sum(BYTES.values()) * S / T
     gbs = chain_bytes * reps / secs / 1e9
     return {

@@ -115,6 +115,17 @@ V7_ABI void v7s_swiglu_row(float *gate_inout, float *up, int hidden);
 typedef void(V7_ABI *v7s_swiglu_quantize_row_fn)(char *out_q, float *gate, float *up, float *out_s, int hidden);
 V7_ABI void v7s_swiglu_quantize_row(char *out_q, float *gate, float *up, float *out_s, int hidden);
 
+/* Replaces the engine-internal v7s_rope_only_heads(buf, n_heads, head_dim,
+ * cos, sin, pos, rope_max_dim), src/asm/rope_only_dispatch.inc:11-47 and
+ * rope_only_kernel.inc:11-53 (no export in src/v7_threading.def; exported
+ * here): RoPE without the per-head RMSNorm, for models without Q/K norm
+ * (PQ_QK_ROPE, src/asm/v7_macros.inc:391-410).  pos == 0 leaves the heads
+ * unchanged.  Contract as v7s_rmsnorm_rope_heads. */
+typedef void(V7_ABI *v7s_rope_only_heads_fn)(float *buf, int n_heads, int head_dim, float *cos_table,
+                                             float *sin_table, int pos, int rope_max_dim);
+V7_ABI void v7s_rope_only_heads(float *buf, int n_heads, int head_dim, float *cos_table, float *sin_table, int pos,
+                                int rope_max_dim);
+
 /* Replaces the engine-internal v7s_kv_pack_f16(dest, src, count),
  * src/asm/kv_f16c.inc:12-52 (no export in src/v7_threading.def; exported
  * here): dest[i] = binary16(src[i]), round to nearest even, for one K or V
@@ -217,6 +228,46 @@ int v7g_qk_rmsnorm_rope(float *q, long long q_token_stride, int n_q_heads, const
                         long long k_token_stride, int n_kv_heads, const float *k_norm_weight, int n_tokens,
                         int head_dim, const float *cos_table, const float *sin_table, const int32_t *positions,
                         int pos0, int rope_max_dim, int table_rows, float eps);
+
+/* RoPE only (no per-head norm) over n_tokens tokens, as v7g_rmsnorm_rope_heads. */
+int v7g_rope_only_heads(float *buf, int n_tokens, long long token_stride, int n_heads, int head_dim,
+                        const float *cos_table, const float *sin_table, const int32_t *positions, int pos0,
+                        int rope_max_dim, int table_rows);
+
+/* The per-token Q/K/V stage of the prefill (src/asm/prefill_q8.inc:848-883:
+ * QKV bias add, Q and K RMSNorm+RoPE or RoPE only, K and V packed to the
+ * binary16 KV cache) for n_tokens tokens in one launch.  Per side: heads of a
+ * token contiguous at buf + t*token_stride; norm_weight NULL = RoPE only (Q,
+ * K) -- V never has one; bias NULL = no bias add; cache NULL = no binary16
+ * rows, else token t's row at cache + t*cache_stride; keep_f32 = 0 (only with
+ * a cache) skips writing the f32 result back.  Q has no cache.  V is
+ * optional (v.buf NULL).  Results equal the reference's per-token calls bit
+ * for bit. */
+typedef struct v7g_qkv_side {
+    float *buf;
+    long long token_stride;
+    int n_heads;
+    const float *norm_weight;
+    const float *bias;
+    uint16_t *cache;
+    long long cache_stride;
+    int keep_f32;
+} v7g_qkv_side;
+
+typedef struct v7g_qkv_stage {
+    v7g_qkv_side q, k, v;
+    int n_tokens;
+    int head_dim;
+    const float *cos_table;
+    const float *sin_table;
+    const int32_t *positions; /* device int32 per token, or NULL: pos0 + t */
+    int pos0;
+    int rope_max_dim;
+    int table_rows;
+    float eps;
+} v7g_qkv_stage;
+
+int v7g_qkv_rope_stage(const v7g_qkv_stage *stage);
 
 /* v7g_qk_rmsnorm_rope that also writes the rotated K heads of token t as
  * binary16 into k_cache + t*k_cache_stride (the v7s_kv_pack_f16 of the K row

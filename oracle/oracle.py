@@ -53,6 +53,8 @@ def lib():
             "orc_rmsnorm_quantize_rows": (None, [_i8p, _f32p, _f32p, _f32p, c_int, c_int, c_int, c_float]),
             "orc_add_inplace": (None, [_f32p, _f32p, c_ll]),
             "orc_kv_pack_f16": (None, [_u16p, _f32p, c_ll]),
+            "orc_rope_only_heads": (None, [_f32p, c_int, c_int, _f32p, _f32p, c_int, c_int]),
+            "orc_bias_add": (None, [_f32p, _f32p, c_ll]),
             "orc_avx2_kv_pack_f16": (None, [_u16p, _f32p, c_ll]),
             "orc_f16c_available": (c_int, []),
             "orc_check_f16_vs_f16c": (ctypes.c_ulonglong, [ctypes.c_uint64, ctypes.c_uint64, c_int]),
@@ -180,6 +182,43 @@ def rmsnorm_quantize(x, weight, eps, gs=64):
     s = np.empty(rows * spr, np.float32)
     lib().orc_rmsnorm_quantize_rows(q, s, x.reshape(-1), _c(weight, np.float32), rows, dim, gs, eps)
     return q.reshape(x.shape), s.reshape(rows, spr)
+
+
+def rope_only(buf, cos_table, sin_table, positions):
+    """v7s_rope_only_heads per token: buf [T, H, D] -> new array."""
+    b = _c(buf, np.float32).copy()
+    T, H, D = b.shape
+    ct = _c(cos_table, np.float32)
+    st = _c(sin_table, np.float32)
+    for t in range(T):
+        lib().orc_rope_only_heads(b[t].reshape(-1), H, D, ct, st, int(positions[t]), ct.shape[-1])
+    return b
+
+
+def bias_add(x, bias):
+    """PQ_BIAS_ADD per token row: x [T, n] + bias [n] -> new array."""
+    x = _c(x, np.float32).copy()
+    b = _c(bias, np.float32).reshape(-1)
+    for row in x.reshape(-1, b.size):
+        lib().orc_bias_add(row, b, b.size)
+    return x
+
+
+def qkv_stage(q, k, v, q_w, k_w, q_bias, k_bias, v_bias, cos_table, sin_table, positions, eps):
+    """Stage C of the Q8 prefill for T tokens (src/asm/prefill_q8.inc:848-883): per side, the bias add
+    (if given), then RMSNorm+RoPE (norm weight given) or RoPE only, for Q and K; V gets the bias only.
+    Returns (q, k, v, k_f16, v_f16) with the binary16 cache rows of K and V (v7s_kv_pack_f16)."""
+    T = q.shape[0]
+    qs, ks, vs = q.shape, k.shape, v.shape
+    q2 = bias_add(q.reshape(T, -1), q_bias).reshape(qs) if q_bias is not None else _c(q, np.float32).copy()
+    k2 = bias_add(k.reshape(T, -1), k_bias).reshape(ks) if k_bias is not None else _c(k, np.float32).copy()
+    v2 = bias_add(v.reshape(T, -1), v_bias).reshape(vs) if v_bias is not None else _c(v, np.float32).copy()
+    pos = np.asarray(positions, np.int32)
+    q2 = rmsnorm_rope(q2, q_w, cos_table, sin_table, pos, eps) if q_w is not None else rope_only(q2, cos_table,
+                                                                                                    sin_table, pos)
+    k2 = rmsnorm_rope(k2, k_w, cos_table, sin_table, pos, eps) if k_w is not None else rope_only(k2, cos_table,
+                                                                                                    sin_table, pos)
+    return q2, k2, v2, kv_pack_f16(k2), kv_pack_f16(v2)
 
 
 def kv_pack_f16(x):

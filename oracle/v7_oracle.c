@@ -442,3 +442,38 @@ void orc_kv_pack_f16(uint16_t *dst, const float *src, long long n)
     for (long long i = 0; i < n; ++i)
         dst[i] = orc_f32_to_f16_bits(src[i]);
 }
+
+/* v7s_rope_only_heads(buf, n_heads, head_dim, cos, sin, pos, rope_max_dim): src/asm/rope_only_dispatch.inc:11-47
+ * (one job per head) and v7s_rope_only_head, src/asm/rope_only_kernel.inc:11-53 (internal in v7; the RoPE of
+ * models without per-head Q/K norm, chosen by PQ_QK_ROPE, src/asm/v7_macros.inc:391-410).  pos == 0 returns
+ * the head unchanged; otherwise each pair (j, j + half) of the head:
+ *   re = lower*cos; ro = lower*sin; re = fma(-upper, sin, re); ro = fma(upper, cos, ro). */
+void orc_rope_only_heads(float *buf, int n_heads, int head_dim, const float *cos_table, const float *sin_table,
+                         int pos, int rope_max_dim)
+{
+    if (pos == 0)
+        return;
+    const float *c = cos_table + (long long)pos * rope_max_dim;
+    const float *s = sin_table + (long long)pos * rope_max_dim;
+    int half = head_dim / 2;
+    for (int h = 0; h < n_heads; ++h) {
+        float *x = buf + (long long)h * head_dim;
+        for (int j = 0; j < half; ++j) {
+            float lo = x[j], up = x[j + half];
+            float re = lo * c[j];
+            float ro = lo * s[j];
+            re = fmaf(-up, s[j], re);
+            ro = fmaf(up, c[j], ro);
+            x[j] = re;
+            x[j + half] = ro;
+        }
+    }
+}
+
+/* PQ_BIAS_ADD (src/asm/v7_macros.inc:366-383): x = x + bias, vaddps, the QKV bias of Stage C
+ * (src/asm/prefill_q8.inc:848-879); n is all_heads_dim or kv_dim. */
+void orc_bias_add(float *x, const float *bias, long long n)
+{
+    for (long long i = 0; i < n; ++i)
+        x[i] = x[i] + bias[i];
+}

@@ -72,6 +72,11 @@ int orc_f16c_available(void);
 void orc_avx2_kv_pack_f16(uint16_t *dst, const float *src, long long n);
 unsigned long long orc_check_f16_vs_f16c(uint64_t lo, uint64_t count, int n_threads);
 
+/* v7s_rope_only_heads (internal in v7): RoPE without the per-head norm, one token; PQ_BIAS_ADD */
+void orc_rope_only_heads(float *buf, int n_heads, int head_dim, const float *cos_table, const float *sin_table,
+                         int pos, int rope_max_dim);
+void orc_bias_add(float *x, const float *bias, long long n);
+
 /* AVX2 restatement (v7_oracle_avx2.c): same results bit for bit, used as the CPU baseline */
 int orc_avx2_available(void);
 void orc_avx2_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int dim, float eps);

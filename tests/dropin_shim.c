@@ -63,3 +63,9 @@ void shim_kv_pack_f16(uint16_t *dest, float *src, int count)
 {
     v7s_kv_pack_f16(dest, src, count);
 }
+
+void shim_rope_only_heads(float *buf, int n_heads, int head_dim, float *cos_table, float *sin_table, int pos,
+                          int rope_max_dim)
+{
+    v7s_rope_only_heads(buf, n_heads, head_dim, cos_table, sin_table, pos, rope_max_dim);
+}

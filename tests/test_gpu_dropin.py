@@ -42,6 +42,7 @@ def shim():
     S.shim_rmsnorm_quantize.argtypes = [vp, vp, vp, i, vp]
     S.shim_add_inplace.argtypes = [vp, vp, i]
     S.shim_kv_pack_f16.argtypes = [vp, vp, i]
+    S.shim_rope_only_heads.argtypes = [vp, i, i, vp, vp, i, i]
     torch.cuda.synchronize()
     L.v7g_set_stream(torch.cuda.current_stream().cuda_stream)
     L.v7g_clear_last_error()
@@ -205,3 +206,14 @@ def test_v7s_kv_pack_f16_row(shim, oracle, count):
     S.shim_kv_pack_f16(ht.data_ptr(), xt.data_ptr(), count)
     done(L)
     assert bits(ht.cpu().numpy().view(np.uint16), oracle.kv_pack_f16(x))
+
+
+@pytest.mark.parametrize("heads,hd,pos", [(1, 64, 0), (4, 64, 7), (16, 128, 31), (8, 96, 5), (8, 128, 4000)])
+def test_v7s_rope_only_heads_per_token(shim, oracle, heads, hd, pos):
+    S, L = shim
+    buf = C.normal(heads * hd + pos, (1, heads, hd))
+    ct, st = oracle.rope_tables(pos + 1, hd, 1e4)
+    bt, ctt, stt = dev(buf), dev(ct), dev(st)
+    S.shim_rope_only_heads(bt.data_ptr(), heads, hd, ctt.data_ptr(), stt.data_ptr(), pos, hd // 2)
+    done(L)
+    assert bits(bt.cpu().numpy(), oracle.rope_only(buf, ct, st, np.array([pos], np.int32)))

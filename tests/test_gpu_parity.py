@@ -438,3 +438,80 @@ def test_qk_rope_with_fused_k_pack(ops, oracle, keep, hd):
     c = host(cache).view(np.uint16)
     assert_bits(c[2:2 + T], oracle.kv_pack_f16(want_k), "k cache")
     assert not c[:2].any() and not c[2 + T:].any()
+
+
+# --------------------------------------------------------------------------- RoPE only, the fused Q/K/V stage
+
+@pytest.mark.parametrize("hd", [64, 96, 128, 256])
+def test_rope_only_heads_tokens(ops, oracle, hd):
+    T, H = 41, 3
+    buf = C.normal(hd + 40, (T, H, hd))
+    ct, st = oracle.rope_tables(64, hd, 1e4)
+    pos = C.rng(hd).integers(0, 64, T).astype(np.int32)
+    pos[0] = 0
+    bt = dev(buf)
+    ops.rope_only_heads(bt, dev(ct), dev(st), positions=dev(pos))
+    assert_bits(host(bt), oracle.rope_only(buf, ct, st, pos), f"rope only hd={hd}")
+
+
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("hd", [128, 96])
+def test_qkv_stage_matches_the_per_token_calls(ops, oracle, norm, bias, hd):
+    """One launch == Stage C of the Q8 prefill per token (src/asm/prefill_q8.inc:848-883): bias add, Q/K
+    RMSNorm+RoPE (Qwen3) or RoPE only (Llama), K and V binary16 cache rows."""
+    T, Hq, Hk = 53, 6, 2
+    w = (Hq + 2 * Hk) * hd
+    qkv = C.normal(hd + 90, (T, w))
+    qw, kw = C.norm_weight(hd + 91, hd), C.norm_weight(hd + 92, hd)
+    qb = C.normal(hd + 93, Hq * hd, 0.5) if bias else None
+    kb = C.normal(hd + 94, Hk * hd, 0.5) if bias else None
+    vb = C.normal(hd + 95, Hk * hd, 0.5) if bias else None
+    ct, st = oracle.rope_tables(T + 10, hd, 1e6)
+    pos = (np.arange(T) + 10).astype(np.int32)
+    pos[3] = 0
+    q_np = qkv[:, :Hq * hd].reshape(T, Hq, hd)
+    k_np = qkv[:, Hq * hd:(Hq + Hk) * hd].reshape(T, Hk, hd)
+    v_np = qkv[:, (Hq + Hk) * hd:].reshape(T, Hk, hd)
+    wq, wk, wv, wkc, wvc = oracle.qkv_stage(q_np, k_np, v_np, qw if norm else None, kw if norm else None, qb, kb, vb,
+                                            ct, st, pos, 1e-6)
+    t = dev(qkv)
+    q = t[:, :Hq * hd].view(T, Hq, hd)
+    k = t[:, Hq * hd:(Hq + Hk) * hd].view(T, Hk, hd)
+    v = t[:, (Hq + Hk) * hd:].view(T, Hk, hd)
+    kc = torch.zeros((T, Hk, hd), dtype=torch.float16, device="cuda")
+    vc = torch.zeros((T, Hk, hd), dtype=torch.float16, device="cuda")
+    d = lambda a: None if a is None else dev(a)  # noqa: E731
+    ops.qkv_rope_stage(q, k, v, dev(ct), dev(st), positions=dev(pos), eps=1e-6,
+                       q_norm_weight=d(qw) if norm else None, k_norm_weight=d(kw) if norm else None,
+                       q_bias=d(qb), k_bias=d(kb), v_bias=d(vb), k_cache=kc, v_cache=vc)
+    out = host(t)
+    assert_bits(out[:, :Hq * hd].reshape(T, Hq, hd), wq, "q")
+    assert_bits(out[:, Hq * hd:(Hq + Hk) * hd].reshape(T, Hk, hd), wk, "k")
+    assert_bits(out[:, (Hq + Hk) * hd:].reshape(T, Hk, hd), wv, "v")
+    assert_bits(host(kc).view(np.uint16), wkc, "k cache")
+    assert_bits(host(vc).view(np.uint16), wvc, "v cache")
+
+
+def test_qkv_stage_cache_only_leaves_f32_k_v(ops, oracle):
+    T, Hq, Hk, hd = 9, 4, 2, 128
+    qkv = C.normal(7, (T, (Hq + 2 * Hk) * hd))
+    ct, st = oracle.rope_tables(T, hd, 1e6)
+    pos = np.arange(T, dtype=np.int32)
+    q_np = qkv[:, :Hq * hd].reshape(T, Hq, hd)
+    k_np = qkv[:, Hq * hd:(Hq + Hk) * hd].reshape(T, Hk, hd)
+    v_np = qkv[:, (Hq + Hk) * hd:].reshape(T, Hk, hd)
+    qw, kw = C.norm_weight(8, hd), C.norm_weight(9, hd)
+    wq, wk, wv, wkc, wvc = oracle.qkv_stage(q_np, k_np, v_np, qw, kw, None, None, None, ct, st, pos, 1e-6)
+    t = dev(qkv)
+    kc = torch.zeros((T, Hk, hd), dtype=torch.float16, device="cuda")
+    vc = torch.zeros((T, Hk, hd), dtype=torch.float16, device="cuda")
+    ops.qkv_rope_stage(t[:, :Hq * hd].view(T, Hq, hd), t[:, Hq * hd:(Hq + Hk) * hd].view(T, Hk, hd),
+                       t[:, (Hq + Hk) * hd:].view(T, Hk, hd), dev(ct), dev(st), positions=dev(pos),
+                       q_norm_weight=dev(qw), k_norm_weight=dev(kw), k_cache=kc, v_cache=vc, keep_k_f32=False,
+                       keep_v_f32=False)
+    out = host(t)
+    assert_bits(out[:, :Hq * hd].reshape(T, Hq, hd), wq, "q")
+    assert_bits(out[:, Hq * hd:], qkv[:, Hq * hd:], "k and v f32 untouched")
+    assert_bits(host(kc).view(np.uint16), wkc, "k cache")
+    assert_bits(host(vc).view(np.uint16), wvc, "v cache")

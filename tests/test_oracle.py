@@ -456,3 +456,44 @@ def test_kv_pack_f16_vs_numpy_and_f16c(oracle):
     assert bits_equal(oracle.kv_pack_f16(x), want)
     if oracle.f16c_available():
         assert bits_equal(oracle.avx2_kv_pack_f16(x), want)
+
+
+# --------------------------------------------------------------------------- RoPE-only heads, QKV bias
+
+def test_rope_only_known_answers(oracle):
+    """pos 0: unchanged; quarter-turn tables: (lo, up) -> (-up, lo) exactly; identity tables: unchanged; and the
+    rotation equals RMSNorm+RoPE's rotation applied to an already-normalised head (w = 1, scale exactly 1)."""
+    T, H, D = 3, 2, 128
+    x = C.normal(1, (T, H, D))
+    ct, st = oracle.rope_tables(8, D, 1e4)
+    assert bits_equal(oracle.rope_only(x, ct, st, np.zeros(T, np.int32)), x)
+    half = D // 2
+    c90 = np.zeros((2, half), F)
+    s90 = np.ones((2, half), F)
+    got = oracle.rope_only(x, c90, s90, np.ones(T, np.int32))
+    assert bits_equal(got[..., :half], -x[..., half:]) and bits_equal(got[..., half:], x[..., :half])
+    got = oracle.rope_only(x, np.ones((2, half), F), np.zeros((2, half), F), np.ones(T, np.int32))
+    assert bits_equal(got, x)
+    # a head whose sum of squares is exactly D (entries +-1) has scale 1/sqrt(1 + 0) = 1 with eps = 0
+    u = np.where(C.normal(2, (T, H, D)) > 0, 1.0, -1.0).astype(F)
+    pos = np.array([1, 5, 7], np.int32)
+    assert bits_equal(oracle.rope_only(u, ct, st, pos), oracle.rmsnorm_rope(u, np.ones(D, F), ct, st, pos, 0.0))
+
+
+def test_rope_only_vs_double(oracle):
+    T, H, D = 16, 4, 128
+    x = C.normal(3, (T, H, D))
+    ct, st = oracle.rope_tables(T, D, 1e6)
+    pos = np.arange(T, dtype=np.int32)
+    got = oracle.rope_only(x, ct, st, pos).astype(np.float64)
+    c = ct[pos].astype(np.float64)[:, None, :]
+    s = st[pos].astype(np.float64)[:, None, :]
+    lo, up = x[..., :D // 2].astype(np.float64), x[..., D // 2:].astype(np.float64)
+    d = np.concatenate([lo * c - up * s, lo * s + up * c], axis=-1)
+    assert np.max(np.abs(got - d)) < 1e-5
+
+
+def test_bias_add_exact(oracle):
+    x = C.normal(4, (5, 1024))
+    b = C.normal(5, 1024)
+    assert bits_equal(oracle.bias_add(x, b), (x + b).astype(F))

@@ -50,6 +50,8 @@ SIGNATURES = {
     "v7g_qk_rmsnorm_rope_kv": (_i, [_vp, _ll, _i, _vp, _vp, _ll, _i, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _i, _f,
                                     _vp, _ll, _i]),
     "v7g_kv_pack_f16": (_i, [_vp, _ll, _vp, _ll, _i, _i]),
+    "v7g_rope_only_heads": (_i, [_vp, _i, _ll, _i, _i, _vp, _vp, _vp, _i, _i, _i]),
+    "v7g_qkv_rope_stage": (_i, [_vp]),
     "v7g_swiglu_f32": (_i, [_vp, _vp, _vp, _ll]),
     "v7g_swiglu_q8": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "v7g_quantize_q8": (_i, [_vp, _vp, _vp, _i, _i, _i]),
@@ -69,7 +71,21 @@ DROP_IN = [
     "v7s_swiglu_quantize_row",
     "v7s_rope_init",
     "v7s_kv_pack_f16",
+    "v7s_rope_only_heads",
 ]
+
+
+class QkvSide(ctypes.Structure):
+    """v7g_qkv_side (include/v7g_lib.h)."""
+    _fields_ = [("buf", _vp), ("token_stride", _ll), ("n_heads", _i), ("norm_weight", _vp), ("bias", _vp),
+                ("cache", _vp), ("cache_stride", _ll), ("keep_f32", _i)]
+
+
+class QkvStage(ctypes.Structure):
+    """v7g_qkv_stage (include/v7g_lib.h)."""
+    _fields_ = [("q", QkvSide), ("k", QkvSide), ("v", QkvSide), ("n_tokens", _i), ("head_dim", _i),
+                ("cos_table", _vp), ("sin_table", _vp), ("positions", _vp), ("pos0", _i), ("rope_max_dim", _i),
+                ("table_rows", _i), ("eps", _f)]
 
 _lib = None
 

@@ -10,6 +10,13 @@
 //   pos  > 0: xe = (x_j*scale)*w_j, xo = (x_{j+h}*scale)*w_{j+h},
 //             out_j = fma(-xo, sin_j, xe*cos_j), out_{j+h} = fma(xo, cos_j, xe*sin_j).
 // cos/sin rows are table + pos*rope_max_dim.
+// The same kernels run the whole Q/K/V stage of a prefill token (src/asm/
+// prefill_q8.inc:848-883) in one pass: per side an optional QKV bias add
+// first (PQ_BIAS_ADD, src/asm/v7_macros.inc:366-383), then RMSNorm+RoPE, or
+// RoPE only when the side has no norm weight (v7s_rope_only_heads,
+// src/asm/rope_only_kernel.inc:11-53: the rotation above applied to x
+// itself), nothing more for V; then the f32 head in place and/or its binary16
+// KV-cache row (v7s_kv_pack_f16, src/asm/kv_f16c.inc).
 //
 // gfx950 layout: 8 lanes per head.  Lane m of a head holds the float4 at
 // x[4m + 32k] for every 32-element block k, so each of the 32 FMA chains (YMM
@@ -28,10 +35,11 @@
 namespace v7g {
 
 struct RopeArgs {
-  RopeSide side[2];
+  RopeSide side[3];
   int n_sides;
-  int heads_per_token;  // side[0].n_heads + side[1].n_heads
-  unsigned n_heads;     // n_tokens * heads_per_token
+  int n_heads0, n_heads01;  // side 0 heads; sides 0 + 1 heads
+  int heads_per_token;      // heads of all sides
+  unsigned n_heads;         // n_tokens * heads_per_token
   int head_dim;
   const float *cos_table;
   const float *sin_table;
@@ -40,19 +48,18 @@ struct RopeArgs {
   int rope_max_dim;
   int table_rows;  // positions available in cos/sin; others give NaN rows
   float eps;
-  uint16_t *k_cache;         // optional: binary16 K rows (token t at k_cache + t*k_cache_stride)
-  long long k_cache_stride;  // binary16 elements between consecutive tokens
-  bool keep_k_f32;           // with k_cache: also write the f32 K heads back in place
 };
 
-// Where head f (flat over tokens x heads) lives, its weights and position.
+// Where head f (flat over tokens x heads of all sides) lives, and what to do with it.
 struct HeadRef {
-  float *x;
-  const float *w;
-  uint16_t *kc;  // binary16 cache address of this head's lane, K side with a cache only
+  float *x;        // this lane's first float of the head
+  const float *w;  // norm weight (lane offset) or nullptr: no RMSNorm
+  const float *b;  // bias (lane offset) or nullptr
+  uint16_t *kc;    // binary16 cache address (lane offset) or nullptr
   int pos;
   bool live;
   bool bad_pos;
+  bool rotate;
   bool write_f32;
 };
 
@@ -62,16 +69,19 @@ __device__ __forceinline__ HeadRef head_ref(const RopeArgs &a, unsigned f, int m
   const unsigned ff = r.live ? f : 0u;
   const unsigned t = ff / (unsigned)a.heads_per_token;
   const int h = (int)(ff - t * (unsigned)a.heads_per_token);
-  const int sd = (a.n_sides > 1 && h >= a.side[0].n_heads) ? 1 : 0;
-  const int hs = h - (sd ? a.side[0].n_heads : 0);
-  r.x = a.side[sd].buf + (size_t)t * (size_t)a.side[sd].token_stride + (size_t)hs * a.head_dim + 4 * m;
-  r.w = a.side[sd].norm_weight + 4 * m;
-  const bool kpack = sd == 1 && a.k_cache != nullptr;
-  r.kc = kpack ? a.k_cache + (size_t)t * (size_t)a.k_cache_stride + (size_t)hs * a.head_dim + 4 * m : nullptr;
-  r.write_f32 = !kpack || a.keep_k_f32;
+  const int sd = h < a.n_heads0 ? 0 : (h < a.n_heads01 ? 1 : 2);
+  const int hs = h - (sd == 0 ? 0 : (sd == 1 ? a.n_heads0 : a.n_heads01));
+  const RopeSide &S = a.side[sd];
+  const size_t in_head = (size_t)hs * a.head_dim + 4 * m;
+  r.x = S.buf + (size_t)t * (size_t)S.token_stride + in_head;
+  r.w = S.norm_weight ? S.norm_weight + 4 * m : nullptr;
+  r.b = S.bias ? S.bias + in_head : nullptr;
+  r.kc = S.cache ? S.cache + (size_t)t * (size_t)S.cache_stride + in_head : nullptr;
+  r.rotate = S.rotate;
+  r.write_f32 = !S.cache || S.keep_f32;
   int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
-  // A position outside the tables cannot be read: its heads become NaN.
-  r.bad_pos = pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
+  // A position outside the tables cannot be read: its rotated heads become NaN.
+  r.bad_pos = S.rotate && pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
   r.pos = r.bad_pos ? 0 : pos;
   return r;
 }
@@ -99,23 +109,46 @@ __device__ __forceinline__ float head_scale(const float4 (&x)[K], int head_dim, 
   return rms_scale(t0 + t2, (float)head_dim, eps);
 }
 
+// Loads the head (streaming) and adds the bias, as PQ_BIAS_ADD does before
+// the norm: x = x + b.
 template <int K>
-__device__ __forceinline__ void normalise(float4 (&xn)[K], const float4 (&x)[K], const float *w_ptr, float s,
-                                          bool bad_pos) {
+__device__ __forceinline__ void load_head(float4 (&x)[K], const HeadRef &h) {
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const float4 w = *reinterpret_cast<const float4 *>(w_ptr + 32 * k);
-    xn[k] = make_float4((x[k].x * s) * w.x, (x[k].y * s) * w.y, (x[k].z * s) * w.z, (x[k].w * s) * w.w);
+    x[k] = h.live ? ld_stream4(h.x + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (h.b) {
+      const float4 b = *reinterpret_cast<const float4 *>(h.b + 32 * k);
+      x[k] = make_float4(x[k].x + b.x, x[k].y + b.y, x[k].z + b.z, x[k].w + b.w);
+    }
   }
-  if (bad_pos) {
+}
+
+// xn = (x * s) * w with the RMS scale of the head, or xn = x without a norm
+// weight; NaN for a rotating head whose position is outside the tables.  The
+// branch on h.w is uniform over the 8 lanes of a head, which are the only
+// lanes the scale's exchanges read.
+template <int K>
+__device__ __forceinline__ void normalise(float4 (&xn)[K], const float4 (&x)[K], const HeadRef &h, int head_dim,
+                                          float eps) {
+  if (h.w) {
+    const float s = head_scale<K>(x, head_dim, eps);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float4 w = *reinterpret_cast<const float4 *>(h.w + 32 * k);
+      xn[k] = make_float4((x[k].x * s) * w.x, (x[k].y * s) * w.y, (x[k].z * s) * w.z, (x[k].w * s) * w.w);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) xn[k] = x[k];
+  }
+  if (h.bad_pos) {
     const float q = __builtin_nanf("");
 #pragma unroll
     for (int k = 0; k < K; ++k) xn[k] = make_float4(q, q, q, q);
   }
 }
 
-// The head's results: f32 in place, and/or binary16 into the K cache row
-// (v7s_kv_pack_f16 of the rotated K, src/asm/forward_q8.inc:345-351, fused).
+// The head's results: f32 in place, and/or binary16 into its cache row.
 template <int K>
 __device__ __forceinline__ void store_head(const HeadRef &h, const float4 (&xn)[K]) {
   if (h.write_f32) {
@@ -141,16 +174,13 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_reg_kernel(RopeArgs a) {
 #pragma unroll
   for (int e = 0; e < HPU; ++e) {
     hr[e] = head_ref(a, unit * HPU + e, m);
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-      x[e][k] = hr[e].live ? ld_stream4(hr[e].x + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    load_head<K>(x[e], hr[e]);
   }
 #pragma unroll
   for (int e = 0; e < HPU; ++e) {
-    const float s = head_scale<K>(x[e], 32 * K, a.eps);
     float4 xn[K];
-    normalise<K>(xn, x[e], hr[e].w, s, hr[e].bad_pos);
-    if (hr[e].pos != 0) {
+    normalise<K>(xn, x[e], hr[e], 32 * K, a.eps);
+    if (hr[e].rotate && hr[e].pos != 0) {
       const size_t row = (size_t)hr[e].pos * (size_t)a.rope_max_dim + 4 * m;
       const float *cr = a.cos_table + row;
       const float *sr = a.sin_table + row;
@@ -171,7 +201,8 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_reg_kernel(RopeArgs a) {
 
 // head_dim % 64 == 32: the partner of element e is e +- HD/2, in another lane;
 // every head of the block (32 of them, HD floats each) goes through LDS.  All
-// threads reach the barrier; the rotation itself is skipped at pos 0.
+// threads reach the barrier; the rotation itself is skipped at pos 0 and for
+// sides that do not rotate.
 template <int K>
 __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
   constexpr int HD = 32 * K;
@@ -181,17 +212,14 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
   const unsigned unit = (blockIdx.x * 256u + threadIdx.x) >> 3;
   const HeadRef hr = head_ref(a, unit, m);
   float4 x[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k)
-    x[k] = hr.live ? ld_stream4(hr.x + 32 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
-  const float s = head_scale<K>(x, HD, a.eps);
+  load_head<K>(x, hr);
   float4 xn[K];
-  normalise<K>(xn, x, hr.w, s, hr.bad_pos);
+  normalise<K>(xn, x, hr, HD, a.eps);
   float *hb = lds + (threadIdx.x >> 3) * HD;
 #pragma unroll
   for (int k = 0; k < K; ++k) *reinterpret_cast<float4 *>(hb + 4 * m + 32 * k) = xn[k];
   __syncthreads();
-  if (hr.pos != 0) {
+  if (hr.rotate && hr.pos != 0) {
     const size_t row = (size_t)hr.pos * (size_t)a.rope_max_dim;
     const float *cr = a.cos_table + row;
     const float *sr = a.sin_table + row;
@@ -228,12 +256,13 @@ static void launch_k(const RopeArgs &a, hipStream_t stream) {
 
 void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int head_dim, const float *cos_table,
                          const float *sin_table, const int32_t *positions, int pos0, int rope_max_dim, int table_rows,
-                         float eps, hipStream_t stream, uint16_t *k_cache, long long k_cache_stride, bool keep_k_f32) {
+                         float eps, hipStream_t stream) {
   RopeArgs a;
   a.n_sides = n_sides;
-  a.side[0] = sides[0];
-  a.side[1] = n_sides > 1 ? sides[1] : sides[0];
-  a.heads_per_token = sides[0].n_heads + (n_sides > 1 ? sides[1].n_heads : 0);
+  for (int i = 0; i < 3; ++i) a.side[i] = sides[i < n_sides ? i : 0];
+  a.n_heads0 = sides[0].n_heads;
+  a.n_heads01 = a.n_heads0 + (n_sides > 1 ? sides[1].n_heads : 0);
+  a.heads_per_token = a.n_heads01 + (n_sides > 2 ? sides[2].n_heads : 0);
   a.n_heads = (unsigned)n_tokens * (unsigned)a.heads_per_token;
   a.head_dim = head_dim;
   a.cos_table = cos_table;
@@ -243,9 +272,6 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.rope_max_dim = rope_max_dim;
   a.table_rows = table_rows;
   a.eps = eps;
-  a.k_cache = n_sides > 1 ? k_cache : nullptr;
-  a.k_cache_stride = k_cache_stride;
-  a.keep_k_f32 = keep_k_f32;
   switch (head_dim / 32) {
     case 2: launch_k<2>(a, stream); break;
     case 3: launch_k<3>(a, stream); break;

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <cstring>
 #include <cmath>
 #include <mutex>
 #include <thread>
@@ -298,21 +299,87 @@ int v7g_qk_rmsnorm_rope_kv(float *q, long long q_token_stride, int n_q_heads, co
                            int head_dim, const float *cos_table, const float *sin_table, const int32_t *positions,
                            int pos0, int rope_max_dim, int table_rows, float eps, uint16_t *k_cache,
                            long long k_cache_stride, int keep_k_f32) {
+  v7g_qkv_stage st;
+  memset(&st, 0, sizeof(st));
+  st.q = {q, q_token_stride, n_q_heads, q_norm_weight, nullptr, nullptr, 0, 1};
+  st.k = {k, k_token_stride, n_kv_heads, k_norm_weight, nullptr, k_cache, k_cache_stride, keep_k_f32};
+  st.n_tokens = n_tokens;
+  st.head_dim = head_dim;
+  st.cos_table = cos_table;
+  st.sin_table = sin_table;
+  st.positions = positions;
+  st.pos0 = pos0;
+  st.rope_max_dim = rope_max_dim;
+  st.table_rows = table_rows;
+  st.eps = eps;
+  if (n_tokens > 0 && !k_cache) return fail(V7G_ERR_NULL);
+  return v7g_qkv_rope_stage(&st);
+}
+
+static int check_stage_side(const v7g_qkv_side &sd, int n_tokens, int head_dim, bool allow_norm, bool allow_cache) {
+  if (sd.n_heads <= 0 || sd.token_stride % 4 != 0) return V7G_ERR_SHAPE;
+  if (n_tokens > 1 && sd.token_stride < (long long)sd.n_heads * head_dim) return V7G_ERR_SHAPE;
+  if ((sd.norm_weight && !allow_norm) || (sd.cache && !allow_cache)) return V7G_ERR_SHAPE;
+  if (!sd.keep_f32 && !sd.cache) return V7G_ERR_SHAPE;  // nothing would be written
+  if (sd.cache && (sd.cache_stride % 4 != 0 || (n_tokens > 1 && sd.cache_stride < (long long)sd.n_heads * head_dim)))
+    return V7G_ERR_SHAPE;
+  if (n_tokens == 0) return V7G_OK;
+  if (!sd.buf) return V7G_ERR_NULL;
+  if (!al16(sd.buf) || (sd.norm_weight && !al16(sd.norm_weight)) || (sd.bias && !al16(sd.bias)) ||
+      ((uintptr_t)sd.cache & 7u))
+    return V7G_ERR_ALIGN;
+  return V7G_OK;
+}
+
+int v7g_qkv_rope_stage(const v7g_qkv_stage *st) {
+  if (!st) return fail(V7G_ERR_NULL);
+  const bool has_v = st->v.buf != nullptr;
+  int rc = check_rope_common(st->n_tokens, st->head_dim, st->cos_table, st->sin_table, st->rope_max_dim,
+                             st->table_rows);
+  if (!rc) rc = check_stage_side(st->q, st->n_tokens, st->head_dim, true, false);
+  if (!rc) rc = check_stage_side(st->k, st->n_tokens, st->head_dim, true, true);
+  if (!rc && has_v) rc = check_stage_side(st->v, st->n_tokens, st->head_dim, false, true);
+  if (!rc) rc = check_rope_heads(st->n_tokens, st->q.n_heads + st->k.n_heads + (has_v ? st->v.n_heads : 0));
+  if (!rc && st->positions && ((uintptr_t)st->positions & 3u)) rc = V7G_ERR_ALIGN;
+  if (rc) return fail(rc);
+  if (st->n_tokens == 0) return V7G_OK;
+  v7g::RopeSide sides[3];
+  const v7g_qkv_side *src[3] = {&st->q, &st->k, &st->v};
+  for (int i = 0; i < 3; ++i) {
+    sides[i].buf = src[i]->buf;
+    sides[i].token_stride = src[i]->token_stride;
+    sides[i].n_heads = src[i]->n_heads;
+    sides[i].norm_weight = src[i]->norm_weight;
+    sides[i].bias = src[i]->bias;
+    sides[i].cache = src[i]->cache;
+    sides[i].cache_stride = src[i]->cache_stride;
+    sides[i].keep_f32 = src[i]->keep_f32 != 0;
+    sides[i].rotate = i < 2;
+  }
+  v7g::launch_rmsnorm_rope(sides, has_v ? 3 : 2, st->n_tokens, st->head_dim, st->cos_table, st->sin_table,
+                           st->positions, st->pos0, st->rope_max_dim, st->table_rows, st->eps, stream());
+  return check_launch();
+}
+
+int v7g_rope_only_heads(float *buf, int n_tokens, long long token_stride, int n_heads, int head_dim,
+                        const float *cos_table, const float *sin_table, const int32_t *positions, int pos0,
+                        int rope_max_dim, int table_rows) {
   int rc = check_rope_common(n_tokens, head_dim, cos_table, sin_table, rope_max_dim, table_rows);
-  if (!rc) rc = check_rope_side(q, q_token_stride, n_q_heads, head_dim, q_norm_weight, n_tokens);
-  if (!rc) rc = check_rope_side(k, k_token_stride, n_kv_heads, head_dim, k_norm_weight, n_tokens);
-  if (!rc) rc = check_rope_heads(n_tokens, n_q_heads + n_kv_heads);
+  if (!rc) {
+    if (n_heads <= 0 || token_stride % 4 != 0 || (n_tokens > 1 && token_stride < (long long)n_heads * head_dim))
+      rc = V7G_ERR_SHAPE;
+    else if (n_tokens > 0 && !buf)
+      rc = V7G_ERR_NULL;
+    else if (n_tokens > 0 && !al16(buf))
+      rc = V7G_ERR_ALIGN;
+  }
+  if (!rc) rc = check_rope_heads(n_tokens, n_heads);
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
-  if (!rc && (k_cache_stride % 4 != 0 || (n_tokens > 1 && k_cache_stride < (long long)n_kv_heads * head_dim)))
-    rc = V7G_ERR_SHAPE;
-  if (!rc && n_tokens > 0 && !k_cache) rc = V7G_ERR_NULL;
-  if (!rc && ((uintptr_t)k_cache & 7u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
-  v7g::RopeSide sides[2] = {{q, q_token_stride, n_q_heads, q_norm_weight},
-                            {k, k_token_stride, n_kv_heads, k_norm_weight}};
-  v7g::launch_rmsnorm_rope(sides, 2, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
-                           table_rows, eps, stream(), k_cache, k_cache_stride, keep_k_f32 != 0);
+  v7g::RopeSide side{buf, token_stride, n_heads, nullptr};
+  v7g::launch_rmsnorm_rope(&side, 1, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
+                           table_rows, 0.0f, stream());
   return check_launch();
 }
 
@@ -381,6 +448,16 @@ int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const 
 
 V7_ABI void v7s_fused_add_rmsnorm(float *o, float *residual, float *add, float *weight, int dim) {
   v7g_fused_add_rmsnorm(o, residual, add, weight, 1, dim, g_eps.load());
+}
+
+V7_ABI void v7s_rope_only_heads(float *buf, int n_heads, int head_dim, float *cos_table, float *sin_table, int pos,
+                                int rope_max_dim) {
+  if (pos < 0) {
+    fail(V7G_ERR_SHAPE);
+    return;
+  }
+  v7g_rope_only_heads(buf, 1, (long long)n_heads * head_dim, n_heads, head_dim, cos_table, sin_table, nullptr, pos,
+                      rope_max_dim, pos + 1);
 }
 
 V7_ABI void v7s_kv_pack_f16(uint16_t *dest, float *src, int count) {

@@ -24,19 +24,22 @@ void launch_rmsnorm_quantize(int8_t *q, float *q_s, float *x, const float *add, 
 // x += y over n floats (n % 4 == 0 on the vector path; any n).
 void launch_add_inplace(float *x, const float *y, long long n, hipStream_t stream);
 
+// One side (Q, K or V) of the per-token head stage.
 struct RopeSide {
-  float *buf;               // first head of token 0
-  long long token_stride;   // floats between consecutive tokens
+  float *buf;                // first head of token 0 (f32, updated in place)
+  long long token_stride;    // floats between consecutive tokens
   int n_heads;
-  const float *norm_weight; // [head_dim]
+  const float *norm_weight;  // [head_dim], or nullptr: no per-head RMSNorm
+  const float *bias = nullptr;       // [n_heads*head_dim] added first, or nullptr
+  uint16_t *cache = nullptr;         // binary16 rows (token t at cache + t*cache_stride), or nullptr
+  long long cache_stride = 0;        // binary16 elements between consecutive tokens
+  bool keep_f32 = true;              // with a cache: also write the f32 result in place
+  bool rotate = true;                // false for V: no RoPE
 };
-// With two sides (Q, K) and k_cache != nullptr, the rotated K heads are also
-// written as binary16 rows of the KV cache (and in place as f32 only if
-// keep_k_f32).
+// Up to three sides (Q, K, V) of n_tokens tokens in one launch.
 void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int head_dim, const float *cos_table,
                          const float *sin_table, const int32_t *positions, int pos0, int rope_max_dim, int table_rows,
-                         float eps, hipStream_t stream, uint16_t *k_cache = nullptr, long long k_cache_stride = 0,
-                         bool keep_k_f32 = true);
+                         float eps, hipStream_t stream);
 
 // binary32 -> binary16 rows (v7s_kv_pack_f16): rows x row_len (row_len % 4 == 0).
 void launch_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long long src_stride, int rows,

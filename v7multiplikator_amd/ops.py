@@ -19,8 +19,12 @@ library the first call raises.
   embedding_gather_q8 <- v7s_embedding_row      (src/asm/forward.inc:13-42)
   rope_tables        <- v7s_rope_init           (src/asm/fused_dispatch.inc:58-76)
   kv_pack_f16        <- v7s_kv_pack_f16         (src/asm/kv_f16c.inc:12-52)
+  rope_only_heads    <- v7s_rope_only_heads     (src/asm/rope_only_dispatch.inc:11-47)
+  qkv_rope_stage     <- the per-token Q/K/V stage of the prefill, one launch (src/asm/prefill_q8.inc:848-883)
 """
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -280,6 +284,68 @@ def embedding_gather_q8(ids: torch.Tensor, table_q: torch.Tensor, table_s: torch
                                              table_s.data_ptr(), dim, vocab)
     _lib.check(rc, "embedding_gather_q8")
     return out
+
+
+def rope_only_heads(buf: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
+                    positions: torch.Tensor | None = None, pos0: int = 0) -> torch.Tensor:
+    """In-place RoPE (no per-head norm) of buf [T, H, D]; tables [P, rope_max_dim]."""
+    _need(buf, torch.float32, "buf", contiguous=False)
+    for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
+        _need(t, torch.float32, n)
+    T, H, D, ts = _heads_view(buf, "buf")
+    _bind(buf)
+    rc = _lib.load().v7g_rope_only_heads(buf.data_ptr(), T, ts, H, D, cos_table.data_ptr(), sin_table.data_ptr(),
+                                         _positions(positions, T, buf.device), int(pos0), cos_table.shape[-1],
+                                         cos_table.shape[0])
+    _lib.check(rc, "rope_only_heads")
+    return buf
+
+
+def _side(buf, norm_weight, bias, cache, keep, name):
+    side = _lib.QkvSide()
+    if buf is None:
+        return side, None
+    _need(buf, torch.float32, name, contiguous=False)
+    T, H, D, ts = _heads_view(buf, name)
+    side.buf, side.token_stride, side.n_heads, side.keep_f32 = buf.data_ptr(), ts, H, int(bool(keep))
+    if norm_weight is not None:
+        _need(norm_weight, torch.float32, f"{name} norm_weight")
+        side.norm_weight = norm_weight.data_ptr()
+    if bias is not None:
+        _need(bias, torch.float32, f"{name} bias")
+        if bias.numel() != H * D:
+            raise ValueError(f"{name} bias must hold heads*head_dim floats")
+        side.bias = bias.data_ptr()
+    if cache is not None:
+        _need(cache, torch.float16, f"{name} cache", contiguous=False)
+        Tc, Hc, Dc, cs = _heads_view(cache, f"{name} cache")
+        if (Tc, Hc, Dc) != (T, H, D):
+            raise ValueError(f"{name} cache must be [tokens, heads, head_dim]")
+        side.cache, side.cache_stride = cache.data_ptr(), cs
+    return side, (T, D)
+
+
+def qkv_rope_stage(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, cos_table: torch.Tensor,
+                   sin_table: torch.Tensor, positions: torch.Tensor | None = None, pos0: int = 0, eps: float = 1e-6,
+                   q_norm_weight=None, k_norm_weight=None, q_bias=None, k_bias=None, v_bias=None, k_cache=None,
+                   v_cache=None, keep_k_f32: bool = True, keep_v_f32: bool = True) -> None:
+    """The Q/K/V stage of a prefill over T tokens in one launch: bias add (optional, per side), Q and K
+    RMSNorm+RoPE (norm weight given) or RoPE only, binary16 K/V cache rows (optional); all in place."""
+    for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
+        _need(t, torch.float32, n)
+    st = _lib.QkvStage()
+    st.q, shq = _side(q, q_norm_weight, q_bias, None, True, "q")
+    st.k, shk = _side(k, k_norm_weight, k_bias, k_cache, keep_k_f32, "k")
+    st.v, shv = _side(v, None, v_bias, v_cache, keep_v_f32, "v")
+    if shq != shk or (shv is not None and shv != shq):
+        raise ValueError("q, k (and v) must have the same tokens and head_dim")
+    T, D = shq
+    st.n_tokens, st.head_dim = T, D
+    st.cos_table, st.sin_table = cos_table.data_ptr(), sin_table.data_ptr()
+    st.positions = _positions(positions, T, q.device) or None
+    st.pos0, st.rope_max_dim, st.table_rows, st.eps = int(pos0), cos_table.shape[-1], cos_table.shape[0], float(eps)
+    _bind(q)
+    _lib.check(_lib.load().v7g_qkv_rope_stage(ctypes.addressof(st)), "qkv_rope_stage")
 
 
 def kv_pack_f16(src: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
