@@ -202,7 +202,8 @@ def cpu_baseline(torch, ops, chain, args):
         t, *_ = run(chunk, cores, r_t, q_t, k_t)
         secs += t
         reps += chunk
-        chunk = max(2, int(chunk * min(4.0, max(1.2, (args.cpu_seconds - secs) / max(t, 1e-6) * 0.5))))
+        per_rep = max(t / chunk, 1e-6)
+        chunk = max(1, min(chunk * 4, int((args.cpu_seconds - secs) / per_rep) + 1))
     chain_bytes = sum(BYTES.values()) * S / T
     gbs = chain_bytes * reps / secs / 1e9
     return {

@@ -9,7 +9,12 @@
 //   v7g_loadtest <libv7g.so> swiglu <rows> <hidden>
 //   v7g_loadtest <libv7g.so> swiglu_q8 <rows> <hidden> [gs]
 //   v7g_loadtest <libv7g.so> embedding <tokens> <vocab> <dim>
+//   v7g_loadtest <libv7g.so> rmsnorm_quantize <rows> <dim> [gs]
+//   v7g_loadtest <libv7g.so> add_rmsnorm_quantize <rows> <dim> [gs]
+//   v7g_loadtest <libv7g.so> kv_pack <tokens> <kv_dim>
+//   v7g_loadtest <libv7g.so> qkv_stage <tokens> <q_heads> <kv_heads> <head_dim>
 //   v7g_loadtest <libv7g.so> configs          (every benchmark configuration below)
+//   v7g_loadtest <libv7g.so> next             (the widened rows at the Qwen3-8B T=8192 shape)
 //   options: --iterations N  --time secs  --no-rotate  --per-row
 //
 // Like the reference harnesses it loads the library with dlopen and resolves
@@ -63,6 +68,10 @@ struct Lib {
   int (*swiglu_f32)(float *, const float *, const float *, long long);
   int (*swiglu_q8)(int8_t *, float *, const float *, const float *, int, int, int);
   int (*embedding_gather_q8)(float *, const int32_t *, int, const int8_t *, const float *, int, int);
+  int (*rmsnorm_quantize)(int8_t *, float *, const float *, const float *, int, int, int, float);
+  int (*add_rmsnorm_quantize)(int8_t *, float *, float *, const float *, const float *, int, int, int, float);
+  int (*kv_pack_f16)(uint16_t *, long long, const float *, long long, int, int);
+  int (*qkv_rope_stage)(const v7g_qkv_stage *);
   v7s_fused_add_rmsnorm_fn v7s_fused_add_rmsnorm;
   v7s_rmsnorm_rope_heads_fn v7s_rmsnorm_rope_heads;
   v7s_swiglu_quantize_row_fn v7s_swiglu_quantize_row;
@@ -97,6 +106,10 @@ int load(const char *path, Lib &L) {
   resolve(L, L.swiglu_f32, "v7g_swiglu_f32");
   resolve(L, L.swiglu_q8, "v7g_swiglu_q8");
   resolve(L, L.embedding_gather_q8, "v7g_embedding_gather_q8");
+  resolve(L, L.rmsnorm_quantize, "v7g_rmsnorm_quantize");
+  resolve(L, L.add_rmsnorm_quantize, "v7g_add_rmsnorm_quantize");
+  resolve(L, L.kv_pack_f16, "v7g_kv_pack_f16");
+  resolve(L, L.qkv_rope_stage, "v7g_qkv_rope_stage");
   resolve(L, L.v7s_fused_add_rmsnorm, "v7s_fused_add_rmsnorm");
   resolve(L, L.v7s_rmsnorm_rope_heads, "v7s_rmsnorm_rope_heads");
   resolve(L, L.v7s_swiglu_quantize_row, "v7s_swiglu_quantize_row");
@@ -375,6 +388,122 @@ void run_embedding(const Lib &L, hipStream_t st, int T, int vocab, int dim, cons
   HIPCHECK(hipFree(tsc));
 }
 
+void run_norm_q8(const Lib &L, hipStream_t st, int rows, int dim, int gs, bool add_first, const Opts &opt) {
+  const size_t n = (size_t)rows * dim;
+  const double scales = (double)rows * (dim / gs) * 4;
+  const double bytes = add_first ? 2.0 * n * 4 + n * 4.0 + n + scales + dim * 4.0 : n * 4.0 + n + scales + dim * 4.0;
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(5);
+  std::vector<float *> x(sets), a(sets), sc(sets);
+  std::vector<int8_t *> q(sets);
+  for (int s = 0; s < sets; ++s) {
+    x[s] = device_fill<float>(n, r, -1.f, 1.f);
+    a[s] = add_first ? device_fill<float>(n, r, -1.f, 1.f) : nullptr;
+    q[s] = device_empty<int8_t>(n);
+    sc[s] = device_empty<float>((size_t)rows * (dim / gs));
+  }
+  float *w = device_fill<float>(dim, r, 0.5f, 1.5f);
+  int iters = 0;
+  const double us = time_calls(L, st, sets, opt, [&](int s) {
+    if (add_first)
+      L.add_rmsnorm_quantize(q[s], sc[s], x[s], a[s], w, rows, dim, gs, 1e-6f);
+    else
+      L.rmsnorm_quantize(q[s], sc[s], x[s], w, rows, dim, gs, 1e-6f);
+  }, &iters);
+  char shape[96];
+  snprintf(shape, sizeof shape, "rows=%d dim=%d gs=%d", rows, dim, gs);
+  report(add_first ? "add_rmsnorm_quantize" : "rmsnorm_quantize", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) {
+    HIPCHECK(hipFree(x[s]));
+    if (a[s]) HIPCHECK(hipFree(a[s]));
+    HIPCHECK(hipFree(q[s]));
+    HIPCHECK(hipFree(sc[s]));
+  }
+  HIPCHECK(hipFree(w));
+}
+
+// K and V rows of a fused QKV row packed to two binary16 cache buffers.
+void run_kv_pack(const Lib &L, hipStream_t st, int T, int kv_dim, const Opts &opt) {
+  const long long ts = 6LL * kv_dim;  // a QKV row of Qwen3-8B shape: Q = 4 kv_dim, K, V
+  const double bytes = 2.0 * T * kv_dim * 4 + 2.0 * T * kv_dim * 2;
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(6);
+  std::vector<float *> qkv(sets);
+  std::vector<uint16_t *> kc(sets), vc(sets);
+  for (int s = 0; s < sets; ++s) {
+    qkv[s] = device_fill<float>((size_t)T * ts, r, -2.f, 2.f);
+    kc[s] = device_empty<uint16_t>((size_t)T * kv_dim);
+    vc[s] = device_empty<uint16_t>((size_t)T * kv_dim);
+  }
+  int iters = 0;
+  const double us = time_calls(L, st, sets, opt, [&](int s) {
+    L.kv_pack_f16(kc[s], kv_dim, qkv[s] + 4LL * kv_dim, ts, T, kv_dim);
+    L.kv_pack_f16(vc[s], kv_dim, qkv[s] + 5LL * kv_dim, ts, T, kv_dim);
+  }, &iters);
+  char shape[96];
+  snprintf(shape, sizeof shape, "tokens=%d kv_dim=%d (K and V, two launches)", T, kv_dim);
+  report("kv_pack_f16", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) {
+    HIPCHECK(hipFree(qkv[s]));
+    HIPCHECK(hipFree(kc[s]));
+    HIPCHECK(hipFree(vc[s]));
+  }
+}
+
+// The per-token Q/K/V stage of the prefill in one launch: Q/K RMSNorm+RoPE,
+// K and V binary16 cache rows, f32 Q kept (K and V f32 not written back).
+void run_qkv_stage(const Lib &L, hipStream_t st, int T, int nq, int nk, int hd, const Opts &opt) {
+  const long long ts = (long long)(nq + 2 * nk) * hd;
+  const double bytes = (double)T * (nq + 2 * nk) * hd * 4 + (double)T * nq * hd * 4 + 2.0 * T * nk * hd * 2 +
+                       2.0 * T * (hd / 2) * 4 + 2.0 * hd * 4;
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(7);
+  std::vector<float *> qkv(sets);
+  std::vector<uint16_t *> kc(sets), vc(sets);
+  for (int s = 0; s < sets; ++s) {
+    qkv[s] = device_fill<float>((size_t)T * ts, r, -1.f, 1.f);
+    kc[s] = device_empty<uint16_t>((size_t)T * nk * hd);
+    vc[s] = device_empty<uint16_t>((size_t)T * nk * hd);
+  }
+  float *qw = device_fill<float>(hd, r, 0.5f, 1.5f), *kw = device_fill<float>(hd, r, 0.5f, 1.5f);
+  float *ct = device_empty<float>((size_t)T * hd / 2), *stb = device_empty<float>((size_t)T * hd / 2);
+  if (L.build_rope_tables(ct, stb, T, hd, 1e6f)) {
+    printf("Fail: rope tables\n");
+    exit(1);
+  }
+  int iters = 0;
+  const double us = time_calls(L, st, sets, opt, [&](int s) {
+    v7g_qkv_stage g;
+    memset(&g, 0, sizeof(g));
+    g.q = {qkv[s], ts, nq, qw, nullptr, nullptr, 0, 1};
+    g.k = {qkv[s] + (size_t)nq * hd, ts, nk, kw, nullptr, kc[s], (long long)nk * hd, 0};
+    g.v = {qkv[s] + (size_t)(nq + nk) * hd, ts, nk, nullptr, nullptr, vc[s], (long long)nk * hd, 0};
+    g.n_tokens = T;
+    g.head_dim = hd;
+    g.cos_table = ct;
+    g.sin_table = stb;
+    g.positions = nullptr;
+    g.pos0 = 0;
+    g.rope_max_dim = hd / 2;
+    g.table_rows = T;
+    g.eps = 1e-6f;
+    L.qkv_rope_stage(&g);
+  }, &iters);
+  char shape[128];
+  snprintf(shape, sizeof shape, "tokens=%d q_heads=%d kv_heads=%d head_dim=%d (Q f32, K/V to f16 cache)", T, nq, nk,
+           hd);
+  report("qkv_rope_stage", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) {
+    HIPCHECK(hipFree(qkv[s]));
+    HIPCHECK(hipFree(kc[s]));
+    HIPCHECK(hipFree(vc[s]));
+  }
+  HIPCHECK(hipFree(qw));
+  HIPCHECK(hipFree(kw));
+  HIPCHECK(hipFree(ct));
+  HIPCHECK(hipFree(stb));
+}
+
 int usage() {
   printf("usage: v7g_loadtest <libv7g.so> fused_add_rmsnorm <rows> <dim> | rmsnorm_rope <tokens> <q_heads> "
          "<kv_heads> <head_dim> | swiglu <rows> <hidden> | swiglu_q8 <rows> <hidden> [gs] | embedding <tokens> "
@@ -422,7 +551,21 @@ int main(int argc, char **argv) {
     run_swiglu(L, st, num(1, 0), num(2, 0), num(3, 32), true, opt);
   else if (k == "embedding" && pos.size() >= 4)
     run_embedding(L, st, num(1, 0), num(2, 0), num(3, 0), opt);
-  else if (k == "configs") {
+  else if (k == "rmsnorm_quantize" && pos.size() >= 3)
+    run_norm_q8(L, st, num(1, 0), num(2, 0), num(3, 64), false, opt);
+  else if (k == "add_rmsnorm_quantize" && pos.size() >= 3)
+    run_norm_q8(L, st, num(1, 0), num(2, 0), num(3, 64), true, opt);
+  else if (k == "kv_pack" && pos.size() >= 3)
+    run_kv_pack(L, st, num(1, 0), num(2, 0), opt);
+  else if (k == "qkv_stage" && pos.size() >= 5)
+    run_qkv_stage(L, st, num(1, 0), num(2, 0), num(3, 0), num(4, 0), opt);
+  else if (k == "next") {
+    // The widened rows at the Qwen3-8B T=8192 shape (dim 4096, 32 Q / 8 KV heads of 128).
+    run_norm_q8(L, st, 8192, 4096, 64, false, opt);
+    run_norm_q8(L, st, 8192, 4096, 64, true, opt);
+    run_kv_pack(L, st, 8192, 1024, opt);
+    run_qkv_stage(L, st, 8192, 32, 8, 128, opt);
+  } else if (k == "configs") {
     // The benchmark configurations: C1 .. C4, then the four kernels of the
     // Qwen3-8B T=8192 per-layer chain (C5a .. C5d).
     run_add_rmsnorm(L, st, 512, 2048, opt);
