@@ -347,7 +347,10 @@ void run_swiglu(const Lib &L, hipStream_t st, int rows, int hidden, int gs, bool
 
 void run_embedding(const Lib &L, hipStream_t st, int T, int vocab, int dim, const Opts &opt) {
   const double bytes = (double)T * 4 + (double)T * dim + (double)T * (dim / 64) * 4 + (double)T * dim * 4;
+  // The id sets rotate on their own, enough of them that the table rows they touch exceed 512 MiB
+  // (the outputs rotate through `sets` buffers as for the other kernels).
   const int sets = sets_for(bytes, opt.rotate);
+  const int id_sets = opt.rotate ? sets_for((double)T * dim * (1.0 + 1.0 / 16), true) : 1;
   Rng r(4);
   int8_t *tq = device_empty<int8_t>((size_t)vocab * dim);
   {
@@ -356,34 +359,34 @@ void run_embedding(const Lib &L, hipStream_t st, int T, int vocab, int dim, cons
     HIPCHECK(hipMemcpy(tq, h.data(), h.size(), hipMemcpyHostToDevice));
   }
   float *tsc = device_fill<float>((size_t)vocab * dim / 64, r, 0.001f, 0.02f);
-  std::vector<int32_t *> ids(sets);
+  std::vector<int32_t *> ids(id_sets);
   std::vector<float *> out(sets);
-  std::vector<std::vector<int32_t>> hids(sets, std::vector<int32_t>(T));
-  for (int s = 0; s < sets; ++s) {
+  std::vector<std::vector<int32_t>> hids(id_sets, std::vector<int32_t>(T));
+  for (int s = 0; s < id_sets; ++s) {
     for (auto &v : hids[s]) v = (int32_t)(r.next() % (uint64_t)vocab);
     ids[s] = device_empty<int32_t>(T);
     HIPCHECK(hipMemcpy(ids[s], hids[s].data(), T * 4, hipMemcpyHostToDevice));
-    out[s] = device_empty<float>((size_t)T * dim);
   }
+  for (int s = 0; s < sets; ++s) out[s] = device_empty<float>((size_t)T * dim);
+  const int cycle = sets * id_sets;  // every (output, id) pairing in turn
   v7g_q8_tensor desc{reinterpret_cast<char *>(tq), tsc};
   int iters = 0;
   double us;
   char shape[96];
   if (opt.per_row) {
-    us = time_calls(L, st, sets, opt, [&](int s) {
-      for (int t = 0; t < T; ++t) L.v7s_embedding_row(out[s] + (size_t)t * dim, hids[s][t], dim, &desc);
+    us = time_calls(L, st, cycle, opt, [&](int s) {
+      for (int t = 0; t < T; ++t) L.v7s_embedding_row(out[s % sets] + (size_t)t * dim, hids[s / sets][t], dim, &desc);
     }, &iters);
     snprintf(shape, sizeof shape, "tokens=%d vocab=%d dim=%d per-token-calls", T, vocab, dim);
   } else {
-    us = time_calls(L, st, sets, opt, [&](int s) { L.embedding_gather_q8(out[s], ids[s], T, tq, tsc, dim, vocab); },
-                    &iters);
+    us = time_calls(L, st, cycle, opt, [&](int s) {
+      L.embedding_gather_q8(out[s % sets], ids[s / sets], T, tq, tsc, dim, vocab);
+    }, &iters);
     snprintf(shape, sizeof shape, "tokens=%d vocab=%d dim=%d", T, vocab, dim);
   }
   report("embedding_gather_q8", shape, iters, us, bytes, sets);
-  for (int s = 0; s < sets; ++s) {
-    HIPCHECK(hipFree(ids[s]));
-    HIPCHECK(hipFree(out[s]));
-  }
+  for (int s = 0; s < id_sets; ++s) HIPCHECK(hipFree(ids[s]));
+  for (int s = 0; s < sets; ++s) HIPCHECK(hipFree(out[s]));
   HIPCHECK(hipFree(tq));
   HIPCHECK(hipFree(tsc));
 }
