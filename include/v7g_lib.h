@@ -19,8 +19,10 @@
  * cuda:N).  The library never allocates on a kernel call; v7s_rope_init /
  * v7g_rope_init are the only entries that allocate (the library-owned
  * cos/sin tables, as the reference's v7s_rope_init owns its tables).
- * Launches are asynchronous on the stream set by v7g_set_stream (default: the
- * null stream); v7g_sync() waits for it.
+ * Launches are asynchronous on the calling host thread's stream, set by
+ * v7g_set_stream (default: the null stream); v7g_sync() waits for it.  Host
+ * threads may drive different streams concurrently; eps (v7g_set_rms_eps) and
+ * the sticky error are process-wide, as the reference's g_rms_eps global is.
  */
 #ifndef V7G_LIB_H
 #define V7G_LIB_H
@@ -148,7 +150,8 @@ V7_ABI void v7s_rope_init(int head_dim, float rope_base);
 /* Initialises the HIP runtime on the current device (optional: every entry
  * initialises lazily).  Returns V7G_OK or V7G_ERR_HIP. */
 int v7g_init(void);
-/* Stream for all subsequent launches (a hipStream_t; NULL = null stream). */
+/* Stream for all subsequent launches from the calling host thread (a
+ * hipStream_t; NULL = null stream). */
 void v7g_set_stream(void *stream);
 void *v7g_get_stream(void);
 /* Waits for the library stream; returns V7G_OK or V7G_ERR_HIP. */

@@ -175,3 +175,23 @@ def test_ops_refuse_host_tensors():
         ops.fused_add_rmsnorm(x, x, torch.ones(64))
     with pytest.raises(TypeError):
         ops.quantize_q8(x.double())
+
+
+def test_stream_binding_is_per_host_thread(L):
+    """v7g_set_stream binds the calling thread's launch stream; another thread keeps its own."""
+    import threading
+
+    seen = {}
+    barrier = threading.Barrier(2)
+
+    def worker(name, value):
+        L.v7g_set_stream(value)
+        barrier.wait()
+        seen[name] = L.v7g_get_stream()
+
+    a = threading.Thread(target=worker, args=("a", 0x1000))
+    b = threading.Thread(target=worker, args=("b", 0x2000))
+    a.start(), b.start()
+    a.join(), b.join()
+    assert seen == {"a": 0x1000, "b": 0x2000}
+    assert L.v7g_get_stream() in (None, 0)  # this thread never set one

@@ -20,7 +20,9 @@
 
 namespace {
 
-std::atomic<hipStream_t> g_stream{nullptr};
+// The launch stream belongs to the calling host thread: threads that drive
+// different streams do not see each other's choice.
+thread_local hipStream_t g_stream = nullptr;
 std::atomic<float> g_eps{1e-6f};
 std::atomic<int> g_err{V7G_OK};
 
@@ -104,7 +106,7 @@ void build_tables_host(std::vector<float> &c, std::vector<float> &s, int n_pos, 
   for (auto &t : th) t.join();
 }
 
-hipStream_t stream() { return g_stream.load(std::memory_order_relaxed); }
+hipStream_t stream() { return g_stream; }
 
 }  // namespace
 
@@ -119,8 +121,8 @@ int v7g_init(void) {
   return V7G_OK;
 }
 
-void v7g_set_stream(void *s) { g_stream.store(reinterpret_cast<hipStream_t>(s)); }
-void *v7g_get_stream(void) { return reinterpret_cast<void *>(g_stream.load()); }
+void v7g_set_stream(void *s) { g_stream = reinterpret_cast<hipStream_t>(s); }
+void *v7g_get_stream(void) { return reinterpret_cast<void *>(g_stream); }
 
 int v7g_sync(void) { return hipStreamSynchronize(stream()) == hipSuccess ? V7G_OK : fail(V7G_ERR_HIP); }
 
