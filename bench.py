@@ -14,8 +14,9 @@ Synthetic data: inputs drawn on the device from a seeded generator
 
 Reported value: whole-chain algorithmic bytes (every tensor read once and
 written once) / wall time, in GB/s.  Per-kernel durations come from HIP events
-recorded on the launch stream inside the timed region; `roofline` reports the
-dominant kernel (SwiGLU -> Q8) against the 8 TB/s HBM peak.  `cpu_baseline`
+bound to the kernels' own dispatch timestamps on the launch stream inside the
+timed region; `roofline` reports the dominant kernel (SwiGLU -> Q8) against the
+8 TB/s HBM peak.  `cpu_baseline`
 times the AVX2 restatement of the reference kernels on the host cores, driven
 per token row as the reference engine drives them, on a bounded sample of the
 same workload; that leg also checks the GPU outputs of the sample bit for bit.
@@ -147,14 +148,14 @@ def cpu_baseline(torch, ops, chain, args):
                                          "w_norm", "normed", "q", "k", "q_w", "k_w", "cos_table", "sin_table",
                                          "gate", "up", "act", "codes", "scales")]
 
-    def run(reps, n_threads, residual, q, k):
+    def run(reps, n_threads, residual, q, k, n=S):
         emb = np.empty((S, DIM), np.float32)
         normed = np.empty((S, DIM), np.float32)
         act = np.empty((S, HIDDEN), np.float32)
         codes = np.empty((S, HIDDEN), np.int8)
         scales = np.empty((S, HIDDEN // GS), np.float32)
         p = lambda a: a.ctypes.data  # noqa: E731
-        a = Args(S, DIM, NQ, NKV, HD, HD // 2, HIDDEN, GS, EPS, p(ids), p(positions), p(table_q), p(table_s), p(emb),
+        a = Args(n, DIM, NQ, NKV, HD, HD // 2, HIDDEN, GS, EPS, p(ids), p(positions), p(table_q), p(table_s), p(emb),
                  p(residual), p(add), p(w_norm), p(normed), p(q), p(k), p(q_w), p(k_w), p(cos_t), p(sin_t), p(gate),
                  p(up), p(act), p(codes), p(scales))
         L.orc_avx2_chain_bench.restype = ctypes.c_double
@@ -194,26 +195,80 @@ def cpu_baseline(torch, ops, chain, args):
                  and np.array_equal(qkv_g[:, :NQ * HD], q_h) and np.array_equal(qkv_g[:, NQ * HD:(NQ + NKV) * HD], k_h)
                  and np.array_equal(hostc(sub.codes), codes_c) and np.array_equal(hostc(sub.scales), scales_c))
 
-    # Timing: a warm repetition, then rounds of repetitions until cpu_seconds of work have been timed.
+    # Timing: a warm repetition, then rounds of repetitions until `seconds` of work have been timed.
     r_t, q_t, k_t = residual0.copy(), q_h.copy(), k_h.copy()
-    run(1, cores, r_t, q_t, k_t)
-    secs, reps, chunk = 0.0, 0, 2
-    while secs < args.cpu_seconds:
-        t, *_ = run(chunk, cores, r_t, q_t, k_t)
-        secs += t
-        reps += chunk
-        per_rep = max(t / chunk, 1e-6)
-        chunk = max(1, min(chunk * 4, int((args.cpu_seconds - secs) / per_rep) + 1))
-    chain_bytes = sum(BYTES.values()) * S / T
-    gbs = chain_bytes * reps / secs / 1e9
+
+    def timed(n_threads, n, seconds):
+        run(1, n_threads, r_t, q_t, k_t, n)
+        secs, reps, chunk = 0.0, 0, 1
+        while secs < seconds:
+            t, *_ = run(chunk, n_threads, r_t, q_t, k_t, n)
+            secs += t
+            reps += chunk
+            per_rep = max(t / chunk, 1e-6)
+            chunk = max(1, min(chunk * 4, int((seconds - secs) / per_rep) + 1))
+        return sum(BYTES.values()) * n / T * reps / secs / 1e9, reps, secs
+
+    gbs, reps, secs = timed(cores, S, args.cpu_seconds)
+    # One host thread, as the reference engine runs these kernels on its caller thread, over a quarter of the
+    # sample (the same rows, still beyond the host caches) for a quarter of the time.
+    n1 = max(1, S // 4)
+    gbs1, reps1, secs1 = timed(1, n1, args.cpu_seconds / 4)
     return {
         "value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
         "sample": f"{S} of the {T} tokens of the same chain (same shapes; working set larger than the host "
                   f"caches; per-row calls as the reference engine makes them), {reps} repetitions in {secs:.1f} s, "
                   f"row-parallel over {cores} host threads; "
                   f"AVX2 restatement of the NASM kernels (oracle/v7_oracle_avx2.c), not the reference binary",
+        "single_thread": {"value": round(gbs1, 3), "unit": "GB/s", "cores": 1,
+                          "sample": f"{n1} tokens, {reps1} repetitions in {secs1:.1f} s"},
+        "cpu_model": cpu_model(),
         "gpu_sample_bit_exact": match,
     }
+
+
+class HipEvents:
+    """Timing events of the HIP runtime, created with hipEventDisableSystemFence (0x20000000)."""
+
+    def __init__(self):
+        import ctypes
+
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.made = []
+
+    def create(self):
+        e = self.ct.c_void_p()
+        rc = self.hip.hipEventCreateWithFlags(self.ct.byref(e), 0x20000000)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+        self.made.append(e)
+        return e
+
+    def elapsed_ms(self, a, b):
+        f = self.ct.c_float()
+        rc = self.hip.hipEventElapsedTime(self.ct.byref(f), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return f.value
+
+    def __del__(self):
+        for e in getattr(self, "made", []):
+            self.hip.hipEventDestroy(e)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -253,39 +308,37 @@ def main():
             fn()
     torch.cuda.synchronize()
 
-    # Timed region: K chain steps back to back.  HIP events bracket only the dominant kernel, on the
-    # stream the kernels are launched on (torch's current stream, which the library binds to);
-    # events between every kernel would add their own gaps to the chain.
-    stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # Timed region: K chain steps back to back.  HIP events on the launch stream (torch's current
+    # stream, which the library binds to) time the dominant kernel of every step.
+    # v7g_time_next_call hands them to that kernel's launch, so no record call sits between the
+    # kernels, and they are created without the system-scope fence, whose cache write-back would
+    # otherwise land inside the measured interval and slow the next kernel.
+    lib = _lib.load()
+    hip = HipEvents()
+    ev = [(hip.create(), hip.create()) for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
         for i, (_, fn) in enumerate(launches):
             if i == dom:
-                ev[s][0].record(stream)
-                fn()
-                ev[s][1].record(stream)
-            else:
-                fn()
+                lib.v7g_time_next_call(ev[s][0], ev[s][1])
+            fn()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    dom_ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
+    dom_ms = sum(hip.elapsed_ms(a, b) for a, b in ev) / args.steps
 
-    # Per-kernel pass (after the timed region, not part of `value`): the same K steps with events
-    # around every kernel, for the per-kernel breakdown.
-    evk = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in launches]
-           for _ in range(args.steps)]
+    # Per-kernel pass (after the timed region, not part of `value`): the same K steps with every
+    # kernel timed the same way, for the per-kernel breakdown.
+    evk = [[(hip.create(), hip.create()) for _ in launches] for _ in range(args.steps)]
     for s in range(args.steps):
         for (_, fn), (a, b) in zip(launches, evk[s]):
-            a.record(stream)
+            lib.v7g_time_next_call(a, b)
             fn()
-            b.record(stream)
     torch.cuda.synchronize()
 
     kern = {}
     for i, (name, _) in enumerate(launches):
-        ms = sum(evk[s][i][0].elapsed_time(evk[s][i][1]) for s in range(args.steps)) / args.steps
+        ms = sum(hip.elapsed_ms(*evk[s][i]) for s in range(args.steps)) / args.steps
         gbs = BYTES[name] / (ms * 1e-3) / 1e9
         kern[name] = {"bytes": BYTES[name], "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                       "frac": round(gbs / HBM_PEAK_GBS, 4)}
@@ -314,7 +367,7 @@ def main():
         "data": "synthetic (seeded device generator, distributions of the benchmark configurations)",
         "config": {"workload": "Qwen3-8B per-layer elementwise chain, T=8192: Q8 embedding gather (151936x4096), "
                                "add+RMSNorm d=4096, RMSNorm+RoPE 32Q/8KV hd128, SwiGLU->Q8 I=12288 GS=32",
-                   "tokens": T, "chain_bytes_per_step": total_bytes, "hbm_fraction_of_peak": round(
+                   "tokens": T, "seed": args.seed, "chain_bytes_per_step": total_bytes, "hbm_fraction_of_peak": round(
                        value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "kernel": DOMINANT, "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -156,6 +156,17 @@ void v7g_set_stream(void *stream);
 void *v7g_get_stream(void);
 /* Waits for the library stream; returns V7G_OK or V7G_ERR_HIP. */
 int v7g_sync(void);
+/* Kernel timing without a profiler (no counterpart in the reference, whose
+ * kernels run on the caller thread).  Arms two hipEvent_t events (timing
+ * enabled) for the next call from this host thread that launches work: they
+ * are handed to hipExtLaunchKernel, `start` with that call's first kernel and
+ * `stop` with its last, so no record call sits between the caller's kernels.
+ * Create them with hipEventDisableSystemFence: an event's default system-scope
+ * fence writes caches back inside the measured interval and slows the next
+ * kernel.  Either may be NULL.  A call that launches nothing (a rejected or
+ * empty call) leaves the pair armed; a launching call disarms it.  Returns
+ * V7G_OK. */
+int v7g_time_next_call(void *start_event, void *stop_event);
 /* eps used by the drop-in norm entries (the reference's g_rms_eps global,
  * src/asm/v7_data.inc:509; default 1e-6). */
 void v7g_set_rms_eps(float eps);

@@ -195,3 +195,14 @@ def test_stream_binding_is_per_host_thread(L):
     a.join(), b.join()
     assert seen == {"a": 0x1000, "b": 0x2000}
     assert L.v7g_get_stream() in (None, 0)  # this thread never set one
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with status 2 and says so, before touching a device."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr

@@ -515,3 +515,35 @@ def test_qkv_stage_cache_only_leaves_f32_k_v(ops, oracle):
     assert_bits(out[:, Hq * hd:], qkv[:, Hq * hd:], "k and v f32 untouched")
     assert_bits(host(kc).view(np.uint16), wkc, "k cache")
     assert_bits(host(vc).view(np.uint16), wvc, "v cache")
+
+
+def test_time_next_call_binds_kernel_timestamps(ops):
+    """v7g_time_next_call: the armed events time exactly the next launching call, from its kernels'
+    own timestamps; a rejected call keeps the pair armed; later calls leave the events alone."""
+    from v7multiplikator_amd import _lib
+    L = _lib.load()
+    torch.cuda.synchronize()
+    L.v7g_set_stream(torch.cuda.current_stream().cuda_stream)
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    b.record(stream)
+    rows, hidden = 2048, 8192
+    g = torch.randn(rows, hidden, device="cuda")
+    u = torch.randn(rows, hidden, device="cuda")
+    q = torch.empty(rows, hidden, dtype=torch.int8, device="cuda")
+    s = torch.empty(rows, hidden // 32, device="cuda")
+    assert L.v7g_time_next_call(a.cuda_event, b.cuda_event) == 0
+    # rejected (group size 0): launches nothing, the pair stays armed
+    assert L.v7g_swiglu_q8(q.data_ptr(), s.data_ptr(), g.data_ptr(), u.data_ptr(), rows, hidden, 0) != 0
+    L.v7g_clear_last_error()
+    assert L.v7g_swiglu_q8(q.data_ptr(), s.data_ptr(), g.data_ptr(), u.data_ptr(), rows, hidden, 32) == 0
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b)
+    # 2048 x 8192 SwiGLU -> Q8 moves 153 MB: between 15 us (10 TB/s) and 10 ms
+    assert 0.015 < ms < 10.0, ms
+    # the pair is disarmed: a further call does not move the events
+    assert L.v7g_swiglu_q8(q.data_ptr(), s.data_ptr(), g.data_ptr(), u.data_ptr(), rows, hidden, 32) == 0
+    torch.cuda.synchronize()
+    assert a.elapsed_time(b) == ms
+    assert L.v7g_get_last_error() == 0

@@ -31,6 +31,7 @@ SIGNATURES = {
     "v7g_set_stream": (None, [_vp]),
     "v7g_get_stream": (_vp, []),
     "v7g_sync": (_i, []),
+    "v7g_time_next_call": (_i, [_vp, _vp]),
     "v7g_set_rms_eps": (None, [_f]),
     "v7g_get_rms_eps": (_f, []),
     "v7g_get_last_error": (_i, []),

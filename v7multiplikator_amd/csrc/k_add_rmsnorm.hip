@@ -177,7 +177,7 @@ static void dispatch_rows(const RowLaunch &L, A... args) {
 template <int TPR, int KMAX>
 struct AddNormOp {
   static void launch(const RowLaunch &L, float *o, float *residual, const float *add, const float *weight, float eps) {
-    hipLaunchKernelGGL((fused_add_rmsnorm_kernel<TPR, KMAX>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, o,
+    enqueue((fused_add_rmsnorm_kernel<TPR, KMAX>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, o,
                        residual, add, weight, L.dim, eps);
   }
 };
@@ -185,7 +185,7 @@ struct AddNormOp {
 template <int TPR, int KMAX>
 struct NormOp {
   static void launch(const RowLaunch &L, float *o, float *x, const float *weight, float eps) {
-    hipLaunchKernelGGL((rmsnorm_kernel<TPR, KMAX>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, o, x, weight, L.dim,
+    enqueue((rmsnorm_kernel<TPR, KMAX>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, o, x, weight, L.dim,
                        eps);
   }
 };
@@ -196,17 +196,17 @@ struct NormQ8Op {
                      float eps, int gs) {
     if (add) {
       if (gs == 32)
-        hipLaunchKernelGGL((add_rmsnorm_quantize_kernel<TPR, KMAX, 32>), dim3(L.rows), dim3(TPR), L.lds(), L.stream,
+        enqueue((add_rmsnorm_quantize_kernel<TPR, KMAX, 32>), dim3(L.rows), dim3(TPR), L.lds(), L.stream,
                            q, q_s, x, add, weight, L.dim, eps);
       else
-        hipLaunchKernelGGL((add_rmsnorm_quantize_kernel<TPR, KMAX, 64>), dim3(L.rows), dim3(TPR), L.lds(), L.stream,
+        enqueue((add_rmsnorm_quantize_kernel<TPR, KMAX, 64>), dim3(L.rows), dim3(TPR), L.lds(), L.stream,
                            q, q_s, x, add, weight, L.dim, eps);
     } else {
       if (gs == 32)
-        hipLaunchKernelGGL((rmsnorm_quantize_kernel<TPR, KMAX, 32>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, q,
+        enqueue((rmsnorm_quantize_kernel<TPR, KMAX, 32>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, q,
                            q_s, x, weight, L.dim, eps);
       else
-        hipLaunchKernelGGL((rmsnorm_quantize_kernel<TPR, KMAX, 64>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, q,
+        enqueue((rmsnorm_quantize_kernel<TPR, KMAX, 64>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, q,
                            q_s, x, weight, L.dim, eps);
     }
   }

@@ -67,7 +67,7 @@ void launch_embedding_gather(float *out, const int32_t *ids, int n_tokens, const
   const unsigned per_block = 256u * kEmbDwords;
   const unsigned bpr = ((unsigned)dim / 4u + per_block - 1u) / per_block;
   const unsigned blocks = (unsigned)n_tokens * bpr;
-  hipLaunchKernelGGL(embedding_gather_q8_kernel, dim3(blocks), dim3(256), 0, stream, out, ids, bpr, table_q, table_s,
+  enqueue(embedding_gather_q8_kernel, dim3(blocks), dim3(256), 0, stream, out, ids, bpr, table_q, table_s,
                      dim, vocab);
 }
 

@@ -28,7 +28,7 @@ void launch_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, l
   const unsigned cpr = (unsigned)row_len / 4u;
   const unsigned long long n = (unsigned long long)rows * cpr;
   const unsigned blocks = (unsigned)((n + 255) / 256);
-  hipLaunchKernelGGL(kv_pack_f16_kernel, dim3(blocks), dim3(256), 0, stream, dst, dst_stride, src, src_stride, cpr,
+  enqueue(kv_pack_f16_kernel, dim3(blocks), dim3(256), 0, stream, dst, dst_stride, src, src_stride, cpr,
                      n);
 }
 

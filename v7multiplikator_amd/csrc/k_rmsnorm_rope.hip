@@ -248,9 +248,9 @@ static void launch_k(const RopeArgs &a, hipStream_t stream) {
   if ((32 * K) % 64 == 0) {
     constexpr int HPU = 1;
     const unsigned units = (a.n_heads + HPU - 1) / HPU;
-    hipLaunchKernelGGL((rmsnorm_rope_reg_kernel<K, HPU>), dim3((units + 31u) / 32u), dim3(256), 0, stream, a);
+    enqueue((rmsnorm_rope_reg_kernel<K, HPU>), dim3((units + 31u) / 32u), dim3(256), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((rmsnorm_rope_lds_kernel<K>), dim3((a.n_heads + 31u) / 32u), dim3(256), 0, stream, a);
+    enqueue((rmsnorm_rope_lds_kernel<K>), dim3((a.n_heads + 31u) / 32u), dim3(256), 0, stream, a);
   }
 }
 

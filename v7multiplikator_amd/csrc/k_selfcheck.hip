@@ -114,7 +114,7 @@ int arith_selfcheck(unsigned long long mismatches[4], hipStream_t stream) {
   unsigned long long *d = nullptr;
   if (hipMalloc(&d, sizeof(unsigned long long) * kCheckBlocks * kChecks) != hipSuccess) return -1;
   for (int w = 0; w < kChecks; ++w)
-    hipLaunchKernelGGL(arith_check_kernel, dim3(kCheckBlocks), dim3(256), 0, stream, w, ranges[w].lo,
+    enqueue(arith_check_kernel, dim3(kCheckBlocks), dim3(256), 0, stream, w, ranges[w].lo,
                        ranges[w].hi - ranges[w].lo, d + (size_t)w * kCheckBlocks);
   std::vector<unsigned long long> h((size_t)kCheckBlocks * kChecks);
   int rc = 0;

@@ -55,9 +55,9 @@ __global__ void swiglu_f32_tail_kernel(float *out, const float *gate, const floa
 void launch_swiglu_f32(float *out, const float *gate, const float *up, long long n, hipStream_t stream) {
   long long n4 = n / 4;
   if (n4 > 0)
-    hipLaunchKernelGGL(swiglu_f32_kernel, dim3(stream_blocks(n4)), dim3(kStreamBlock), 0, stream, out, gate, up, n4);
+    enqueue(swiglu_f32_kernel, dim3(stream_blocks(n4)), dim3(kStreamBlock), 0, stream, out, gate, up, n4);
   if (n % 4)
-    hipLaunchKernelGGL(swiglu_f32_tail_kernel, dim3(1), dim3(4), 0, stream, out, gate, up, n4 * 4, n);
+    enqueue(swiglu_f32_tail_kernel, dim3(1), dim3(4), 0, stream, out, gate, up, n4 * 4, n);
 }
 
 // v7s_add_inplace (src/asm/add_kernel.inc:26-49): x = x + y, one vaddps per
@@ -79,8 +79,8 @@ __global__ void add_inplace_tail_kernel(float *x, const float *y, long long star
 void launch_add_inplace(float *x, const float *y, long long n, hipStream_t stream) {
   long long n4 = n / 4;
   if (n4 > 0)
-    hipLaunchKernelGGL(add_inplace_kernel, dim3(stream_blocks(n4)), dim3(kStreamBlock), 0, stream, x, y, n4);
-  if (n % 4) hipLaunchKernelGGL(add_inplace_tail_kernel, dim3(1), dim3(4), 0, stream, x, y, n4 * 4, n);
+    enqueue(add_inplace_kernel, dim3(stream_blocks(n4)), dim3(kStreamBlock), 0, stream, x, y, n4);
+  if (n % 4) enqueue(add_inplace_tail_kernel, dim3(1), dim3(4), 0, stream, x, y, n4 * 4, n);
 }
 
 // Flat path: every row length is a multiple of GS, so groups tile the flat
@@ -150,10 +150,10 @@ static void launch_flat(int8_t *out_q, float *out_s, const float *x, const float
   const long long n4 = n / 4;
   const dim3 grid(stream_blocks(n4));
   if (gate)
-    hipLaunchKernelGGL((quantize_q8_flat_kernel<GS, true>), grid, dim3(kStreamBlock), 0, stream, out_q, out_s, x, gate,
+    enqueue((quantize_q8_flat_kernel<GS, true>), grid, dim3(kStreamBlock), 0, stream, out_q, out_s, x, gate,
                        up, n4);
   else
-    hipLaunchKernelGGL((quantize_q8_flat_kernel<GS, false>), grid, dim3(kStreamBlock), 0, stream, out_q, out_s, x,
+    enqueue((quantize_q8_flat_kernel<GS, false>), grid, dim3(kStreamBlock), 0, stream, out_q, out_s, x,
                        gate, up, n4);
 }
 
@@ -174,10 +174,10 @@ void launch_quantize_q8(int8_t *out_q, float *out_s, const float *x, const float
   const long long groups = (long long)rows * ((row_len + gs - 1) / gs);
   const unsigned blocks = (unsigned)((groups + 255) / 256);
   if (gate)
-    hipLaunchKernelGGL((quantize_q8_generic_kernel<true>), dim3(blocks), dim3(256), 0, stream, out_q, out_s, x, gate,
+    enqueue((quantize_q8_generic_kernel<true>), dim3(blocks), dim3(256), 0, stream, out_q, out_s, x, gate,
                        up, rows, row_len, gs);
   else
-    hipLaunchKernelGGL((quantize_q8_generic_kernel<false>), dim3(blocks), dim3(256), 0, stream, out_q, out_s, x, gate,
+    enqueue((quantize_q8_generic_kernel<false>), dim3(blocks), dim3(256), 0, stream, out_q, out_s, x, gate,
                        up, rows, row_len, gs);
 }
 

@@ -41,7 +41,10 @@ int fail(int code) {
   return code;
 }
 
+// Called after the launches of every launching entry: also disarms the timing
+// events, which cover that one call.
 int check_launch() {
+  v7g::launch_events() = v7g::LaunchEvents{};
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? V7G_OK : fail(V7G_ERR_HIP);
 }
@@ -110,6 +113,13 @@ hipStream_t stream() { return g_stream; }
 
 }  // namespace
 
+namespace v7g {
+LaunchEvents &launch_events() {
+  static thread_local LaunchEvents ev;
+  return ev;
+}
+}  // namespace v7g
+
 extern "C" {
 
 // ---------------------------------------------------------------- control
@@ -123,6 +133,12 @@ int v7g_init(void) {
 
 void v7g_set_stream(void *s) { g_stream = reinterpret_cast<hipStream_t>(s); }
 void *v7g_get_stream(void) { return reinterpret_cast<void *>(g_stream); }
+
+int v7g_time_next_call(void *start_event, void *stop_event) {
+  v7g::launch_events() = v7g::LaunchEvents{reinterpret_cast<hipEvent_t>(start_event),
+                                           reinterpret_cast<hipEvent_t>(stop_event)};
+  return V7G_OK;
+}
 
 int v7g_sync(void) { return hipStreamSynchronize(stream()) == hipSuccess ? V7G_OK : fail(V7G_ERR_HIP); }
 
@@ -192,7 +208,9 @@ int v7g_rope_init(int head_dim, float rope_base, int n_pos) {
 
 int v7g_arith_selfcheck(unsigned long long *mismatches) {
   if (!mismatches) return fail(V7G_ERR_NULL);
-  return v7g::arith_selfcheck(mismatches, stream()) == 0 ? V7G_OK : fail(V7G_ERR_HIP);
+  const int rc = v7g::arith_selfcheck(mismatches, stream());
+  v7g::launch_events() = v7g::LaunchEvents{};
+  return rc == 0 ? V7G_OK : fail(V7G_ERR_HIP);
 }
 
 int v7g_get_rope_tables(float **cos_table, float **sin_table, int *rope_max_dim, int *n_pos) {

@@ -1,9 +1,29 @@
 // v7g_internal.h -- launchers shared between the kernel files and the C-ABI layer.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace v7g {
+
+// Timing events armed by v7g_time_next_call for the calling host thread.  The
+// first kernel of the next launching call takes `start`; every kernel of that
+// call takes `stop`, so the last one sets it.  The API layer disarms the pair
+// after the call.
+struct LaunchEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+LaunchEvents &launch_events();
+
+// Every kernel of the library is enqueued through this helper.
+template <typename... KArgs, typename... Args>
+inline void enqueue(void (*kernel)(KArgs...), dim3 grid, dim3 block, unsigned lds_bytes, hipStream_t stream,
+                   Args... args) {
+  LaunchEvents &ev = launch_events();
+  hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, stream, ev.start, ev.stop, 0u, args...);
+  ev.start = nullptr;
+}
 
 // Launchers: shapes and pointers are validated by the caller (v7g_api.hip);
 // each launcher only computes the grid and enqueues on `stream`.
