@@ -299,8 +299,8 @@ def test_quantize_non_finite(ops, oracle):
 @pytest.mark.parametrize("gs", [32, 64])
 @pytest.mark.parametrize("rows,hidden", [(1, 64), (3, 192), (16, 8192), (5, 96)])
 def test_swiglu_q8_shapes(ops, oracle, gs, rows, hidden):
-    if hidden % gs:
-        pytest.skip("hidden must be a multiple of gs on this path")
+    # hidden 96 with gs 64: each row ends in a 32-element tail group, quantized on its own as the
+    # reference's scalar tail does (src/asm/quantize_kernel.inc:119-152)
     g = C.normal(rows + hidden, (rows, hidden), 1.5)
     u = C.normal(rows + hidden + 1, (rows, hidden), 1.5)
     wq, ws = oracle.swiglu_q8(g, u, gs)

@@ -1,0 +1,157 @@
+"""GPU parity over seeded random shapes: every batched entry against the oracle, bit for bit.
+
+The fixed-shape tests pin the benchmark configurations and the reference validators' shapes; this
+sweep draws the shape parameters at random inside each entry's contract (rows, row lengths that are
+not multiples of the vector width, ragged quantization tails, every head_dim class, tables wider than
+head_dim / 2, positions anywhere in the table) so that an indexing mistake that only shows at an
+unusual shape fails here.  Each case names its parameters in the failure message.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests import common as C
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+CASES = 12
+
+
+@pytest.fixture(scope="module")
+def ops():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a visible MI355X")
+    from v7multiplikator_amd import _lib
+    from v7multiplikator_amd import ops as _ops
+    _lib.load()
+    return _ops
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def same(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    if a.shape != b.shape:
+        return False
+    if a.dtype.kind == "f":
+        return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    return np.array_equal(a, b)
+
+
+def shapes(tag, draw):
+    """CASES parameter sets from a generator seeded by the test's tag."""
+    r = np.random.default_rng(sum(map(ord, tag)) * 7919)
+    return [draw(r) for _ in range(CASES)]
+
+
+def test_sweep_fused_add_rmsnorm(ops, oracle):
+    for rows, dim, eps in shapes("arn", lambda r: (int(r.integers(1, 48)), 8 * int(r.integers(1, 2049)),
+                                                   float(r.choice([1e-6, 1e-5])))):
+        res = C.normal(rows * 7 + dim, (rows, dim))
+        add = C.normal(rows * 7 + dim + 1, (rows, dim))
+        w = C.norm_weight(dim, dim)
+        want_o, want_r = oracle.fused_add_rmsnorm(res, add, w, eps)
+        rt = dev(res)
+        got_o = host(ops.fused_add_rmsnorm(rt, dev(add), dev(w), eps=eps))
+        assert same(got_o, want_o) and same(host(rt), want_r), (rows, dim, eps)
+
+
+def test_sweep_rmsnorm_and_quantize(ops, oracle):
+    for rows, dim, gs, eps in shapes("rmsq", lambda r: (int(r.integers(1, 40)), 64 * int(r.integers(1, 257)),
+                                                        int(r.choice([32, 64])), float(r.choice([1e-6, 1e-5])))):
+        x = C.normal(rows * 13 + dim, (rows, dim), 2.0)
+        w = C.norm_weight(dim + 3, dim)
+        assert same(host(ops.rmsnorm(dev(x), dev(w), eps=eps)), oracle.rmsnorm(x, w, eps)), (rows, dim, eps)
+        wq, ws = oracle.rmsnorm_quantize(x, w, eps, gs)
+        gq, gsc = ops.rmsnorm_quantize(dev(x), dev(w), eps=eps, gs=gs)
+        assert same(host(gq), wq) and same(host(gsc), ws), (rows, dim, gs, eps)
+        add = C.normal(rows * 13 + dim + 1, (rows, dim))
+        rt = dev(x)
+        gq, gsc = ops.add_rmsnorm_quantize(rt, dev(add), dev(w), eps=eps, gs=gs)
+        summed = oracle.add_inplace(x, add)
+        wq, ws = oracle.rmsnorm_quantize(summed, w, eps, gs)
+        assert same(host(rt), summed) and same(host(gq), wq) and same(host(gsc), ws), ("add", rows, dim, gs, eps)
+
+
+def test_sweep_rmsnorm_rope(ops, oracle):
+    def draw(r):
+        hd = 32 * int(r.integers(2, 17))
+        wide = bool(r.integers(0, 2))
+        return int(r.integers(1, 24)), int(r.integers(1, 41)), hd, wide, int(r.integers(1, 300))
+
+    for T, H, hd, wide, n_pos in shapes("rope", draw):
+        table_hd = 2 * hd if wide else hd  # a wider table row than head_dim / 2 is allowed
+        ct, st = oracle.rope_tables(n_pos, table_hd, 1e6 if hd % 64 == 0 else 1e4)
+        pos = C.rng(T * H + hd).integers(0, n_pos, T).astype(np.int32)
+        buf = C.normal(T + H + hd, (T, H, hd))
+        w = C.norm_weight(hd + 5, hd)
+        bt = dev(buf)
+        ops.rmsnorm_rope_heads(bt, dev(w), dev(ct), dev(st), positions=dev(pos), eps=1e-6)
+        assert same(host(bt), oracle.rmsnorm_rope(buf, w, ct, st, pos, 1e-6)), (T, H, hd, wide, n_pos)
+        bt = dev(buf)
+        ops.rope_only_heads(bt, dev(ct), dev(st), positions=dev(pos))
+        assert same(host(bt), oracle.rope_only(buf, ct, st, pos)), ("rope only", T, H, hd, wide, n_pos)
+
+
+def test_sweep_qk_in_fused_row(ops, oracle):
+    """Q and K heads at random offsets inside one token row with a random (wider) token stride."""
+    def draw(r):
+        return (int(r.integers(1, 20)), int(r.integers(1, 17)), int(r.integers(1, 9)), 32 * int(r.integers(2, 9)),
+                4 * int(r.integers(0, 9)))
+
+    for T, nq, nkv, hd, pad in shapes("qk", draw):
+        row = (nq + 2 * nkv) * hd + pad
+        qkv = C.normal(T * row, (T, row))
+        ct, st = oracle.rope_tables(T + 3, hd, 1e6)
+        pos = np.arange(3, T + 3, dtype=np.int32)
+        qw, kw = C.norm_weight(hd, hd), C.norm_weight(hd + 1, hd)
+        t = dev(qkv)
+        q = t[:, :nq * hd].view(T, nq, hd)
+        k = t[:, nq * hd:(nq + nkv) * hd].view(T, nkv, hd)
+        ops.qk_rmsnorm_rope(q, k, dev(qw), dev(kw), dev(ct), dev(st), positions=dev(pos), eps=1e-6)
+        out = host(t)
+        want_q = oracle.rmsnorm_rope(qkv[:, :nq * hd].reshape(T, nq, hd), qw, ct, st, pos, 1e-6)
+        want_k = oracle.rmsnorm_rope(qkv[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd), kw, ct, st, pos, 1e-6)
+        assert same(out[:, :nq * hd].reshape(T, nq, hd), want_q), (T, nq, nkv, hd, pad)
+        assert same(out[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd), want_k), (T, nq, nkv, hd, pad)
+        assert same(out[:, (nq + nkv) * hd:], qkv[:, (nq + nkv) * hd:]), (T, nq, nkv, hd, pad)
+
+
+def test_sweep_swiglu_and_quantize(ops, oracle):
+    def draw(r):
+        return int(r.integers(1, 33)), int(r.integers(1, 5000)), int(r.choice([32, 64]))
+
+    for rows, n, gs in shapes("swq", draw):
+        g = C.normal(rows + n, (rows, n), 1.5)
+        u = C.normal(rows + n + 1, (rows, n), 1.5)
+        assert same(host(ops.swiglu(dev(g), dev(u))), oracle.swiglu(g, u)), ("swiglu", rows, n)
+        wq, ws = oracle.swiglu_q8(g, u, gs)
+        gq, gsc = ops.swiglu_q8(dev(g), dev(u), gs=gs)
+        assert same(host(gq), wq) and same(host(gsc), ws), ("swiglu_q8", rows, n, gs)
+        wq, ws = oracle.quantize(g, gs)
+        gq, gsc = ops.quantize_q8(dev(g), gs=gs)
+        assert same(host(gq), wq) and same(host(gsc), ws), ("quantize", rows, n, gs)
+
+
+def test_sweep_embedding_and_kv_pack(ops, oracle):
+    def draw(r):
+        return int(r.integers(1, 3000)), 64 * int(r.integers(1, 97)), int(r.integers(1, 200))
+
+    for vocab, dim, n in shapes("emb", draw):
+        tq, ts = C.q8_table(vocab + dim, vocab, dim)
+        ids = C.rng(n + vocab).integers(0, vocab, n).astype(np.int32)
+        got = host(ops.embedding_gather_q8(dev(ids), dev(tq), dev(ts)))
+        assert same(got, oracle.embedding_gather(ids, tq, ts, dim)), (vocab, dim, n)
+        x = C.normal(n + dim, (n, dim), 8.0)
+        h = host(ops.kv_pack_f16(dev(x))).view(np.uint16)
+        assert same(h, oracle.kv_pack_f16(x)), ("kv_pack", n, dim)
