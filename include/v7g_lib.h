@@ -304,11 +304,13 @@ int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long 
 int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n);
 
 /* SwiGLU -> Q8: rows x hidden, group size gs (32 or 64, or any 1..4096 on the
- * general path); out_q [rows*hidden] int8, out_s [rows, ceil(hidden/gs)] f32. */
+ * general path); out_q [rows*hidden] int8, out_s [rows, ceil(hidden/gs)] f32
+ * (4-byte aligned).  Groups never cross rows; a row's last group may be
+ * partial.  rows * ceil(hidden/gs) < 2^38. */
 int v7g_swiglu_q8(int8_t *out_q, float *out_s, const float *gate, const float *up, int rows, int hidden, int gs);
 
 /* Q8 block quantization of rows x row_len floats (v7d_quantize per row),
- * scales [rows, ceil(row_len/gs)]. */
+ * scales [rows, ceil(row_len/gs)]; the same contract as v7g_swiglu_q8. */
 int v7g_quantize_q8(int8_t *out_q, float *out_s, const float *x, int rows, int row_len, int gs);
 
 /* Q8 embedding gather: out[t, :] = dequant(table row ids[t]) for n_tokens ids

@@ -55,6 +55,14 @@ def test_library_exports_every_declared_symbol(L):
         assert getattr(L, n) is not None
 
 
+def test_library_exports_only_the_c_abi():
+    """The kernels and C++ launchers are internal: every exported function is a declared C entry."""
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = sorted(line.split()[-1] for line in out.splitlines() if " T " in line)
+    assert exported == declared_functions()
+
+
 def test_python_binding_covers_the_plain_c_entries():
     plain = [n for n in declared_functions() if n.startswith("v7g_")]
     assert sorted(plain) == sorted(_lib.SIGNATURES)
@@ -126,6 +134,9 @@ def test_quantize_and_swiglu_reject(L):
     assert _sticky(L, L.v7g_quantize_q8, FAKE, FAKE, FAKE, 1, 64, 8192)[0] == 2
     assert _sticky(L, L.v7g_quantize_q8, None, FAKE, FAKE, 1, 64, 64)[0] == 1
     assert _sticky(L, L.v7g_swiglu_q8, FAKE, FAKE, None, FAKE, 1, 64, 32)[0] == 1
+    assert _sticky(L, L.v7g_quantize_q8, FAKE, FAKE + 2, FAKE, 1, 64, 64)[0] == 3  # scales 4-byte aligned
+    # gs 1 over 2^38 groups would need more than 2^30 blocks on the general path
+    assert _sticky(L, L.v7g_quantize_q8, FAKE, FAKE, FAKE, 1 << 20, 1 << 18, 1)[0] == 2
     assert _sticky(L, L.v7g_swiglu_f32, FAKE, FAKE, FAKE, -1)[0] == 2
     assert _sticky(L, L.v7g_swiglu_f32, FAKE, FAKE + 8, FAKE, 16)[0] == 3
     assert _sticky(L, L.v7g_swiglu_f32, None, None, None, 0) == (0, 0)

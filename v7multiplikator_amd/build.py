@@ -42,7 +42,9 @@ def sources():
 def build_library(verbose: bool = False) -> str:
     """Compiles every csrc/*.hip into libv7g.so; returns its path."""
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *sources()]
+    exports = os.path.join(CSRC, "v7g_exports.map")
+    cmd = [hipcc(), *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), f"-Wl,--version-script={exports}", "-o", tmp,
+           *sources()]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -178,8 +178,9 @@ int v7g_rope_init(int head_dim, float rope_base, int n_pos) {
     return fail(V7G_ERR_SHAPE);
   std::lock_guard<std::mutex> lk(g_rope_mu);
   if (g_rope_cos) {
-    // Stream-ordered release: launches already queued may still read them.
-    if (hipStreamSynchronize(stream()) != hipSuccess) return fail(V7G_ERR_HIP);
+    // Launches already queued, on any host thread's stream, may still read
+    // the old tables: wait for the whole device before releasing them.
+    if (hipDeviceSynchronize() != hipSuccess) return fail(V7G_ERR_HIP);
     (void)hipFree(g_rope_cos);
     (void)hipFree(g_rope_sin);
     g_rope_cos = g_rope_sin = nullptr;
@@ -428,8 +429,11 @@ int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n) 
 static int check_quant(const int8_t *out_q, const float *out_s, int rows, int row_len, int gs) {
   if (rows < 0 || row_len <= 0 || gs < 1 || gs > 4096) return V7G_ERR_SHAPE;
   if ((long long)rows * row_len >= (1LL << 40)) return V7G_ERR_SHAPE;
+  // the general path runs one thread per group in 256-thread blocks: at most 2^30 blocks
+  if ((long long)rows * ((row_len + gs - 1) / gs) >= (1LL << 38)) return V7G_ERR_SHAPE;
   if (rows == 0) return V7G_OK;
   if (!out_q || !out_s) return V7G_ERR_NULL;
+  if ((uintptr_t)out_s & 3u) return V7G_ERR_ALIGN;
   return V7G_OK;
 }
 
