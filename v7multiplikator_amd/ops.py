@@ -34,18 +34,24 @@ Q8_EMBED_GS = 64  # scale group of the Q8 embedding table (src/asm/forward.inc:1
 
 
 def _bind(t: torch.Tensor) -> None:
+    """Binds the calling thread's library stream to torch's current stream of t's device."""
     if not t.is_cuda:
         raise ValueError("v7g kernels take device tensors (cuda:N)")
     _lib.load().v7g_set_stream(torch.cuda.current_stream(t.device).cuda_stream)
 
 
 def _need(t: torch.Tensor, dtype, name: str, contiguous: bool = True) -> None:
+    """Every tensor of a call lives on the current device, where the library launches."""
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
     if not t.is_cuda:
         raise ValueError(f"{name} must be on a cuda device")
+    cur = torch.cuda.current_device()
+    if t.device.index != cur:
+        raise ValueError(f"{name} is on {t.device} but the current device is cuda:{cur}; "
+                         f"call under torch.cuda.device({t.device})")
     if contiguous and not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
 
