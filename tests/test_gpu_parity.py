@@ -547,3 +547,43 @@ def test_time_next_call_binds_kernel_timestamps(ops):
     torch.cuda.synchronize()
     assert a.elapsed_time(b) == ms
     assert L.v7g_get_last_error() == 0
+
+
+def test_host_threads_drive_their_own_streams(ops, oracle):
+    """Two host threads, each on its own stream (the library binds the stream per thread), run SwiGLU->Q8 and
+    add+RMSNorm concurrently; every result equals the oracle bit for bit."""
+    import threading
+
+    g = C.normal(7001, (64, 4096), 1.5)
+    u = C.normal(7002, (64, 4096), 1.5)
+    res = C.normal(7003, (64, 4096))
+    add = C.normal(7004, (64, 4096))
+    w = C.norm_weight(7005, 4096)
+    want_q, want_s = oracle.swiglu_q8(g, u, 32)
+    want_o, want_r = oracle.fused_add_rmsnorm(res, add, w, 1e-6)
+    errors = []
+
+    def worker(kind):
+        try:
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                for _ in range(20):
+                    if kind == "q8":
+                        q, s = ops.swiglu_q8(dev(g), dev(u), gs=32)
+                        stream.synchronize()
+                        assert np.array_equal(q.cpu().numpy(), want_q) and np.array_equal(s.cpu().numpy(), want_s)
+                    else:
+                        r = dev(res)
+                        o = ops.fused_add_rmsnorm(r, dev(add), dev(w), eps=1e-6)
+                        stream.synchronize()
+                        assert np.array_equal(o.cpu().numpy(), want_o) and np.array_equal(r.cpu().numpy(), want_r)
+        except BaseException as e:  # noqa: BLE001 -- reported by the main thread
+            errors.append((kind, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in ("q8", "norm")]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors
