@@ -587,3 +587,62 @@ def test_host_threads_drive_their_own_streams(ops, oracle):
         t.join(timeout=60)
     assert not any(t.is_alive() for t in threads)
     assert not errors, errors
+
+
+def test_chain_captured_in_a_hip_graph(ops, oracle):
+    """The four chain kernels captured in one HIP graph (torch.cuda.graph) and replayed three times, with eager
+    work between the replays: every replay equals the eager run bit for bit.  The kernels use no memset nodes
+    and allocate nothing, so they are safe to capture."""
+    T, D, V, NQ, NKV, HD, HID = 64, 512, 1000, 4, 2, 128, 1024
+    tq, ts = C.q8_table(8101, V, D)
+    ids = dev(C.rng(8102).integers(0, V, T).astype(np.int32))
+    res0 = dev(C.normal(8103, (T, D)))
+    add = dev(C.normal(8104, (T, D)))
+    w = dev(C.norm_weight(8105, D))
+    qkv0 = dev(C.normal(8106, (T, (NQ + 2 * NKV) * HD)))
+    qw, kw = dev(C.norm_weight(8107, HD)), dev(C.norm_weight(8108, HD))
+    ct, st = (dev(a) for a in oracle.rope_tables(T, HD, 1e6))
+    pos = dev(np.arange(T, dtype=np.int32))
+    gate, up = dev(C.normal(8109, (T, HID), 1.5)), dev(C.normal(8110, (T, HID), 1.5))
+    tqd, tsd = dev(tq), dev(ts)
+    emb = torch.empty((T, D), device="cuda")
+    normed = torch.empty((T, D), device="cuda")
+    codes = torch.empty((T, HID), dtype=torch.int8, device="cuda")
+    scales = torch.empty((T, HID // 32), device="cuda")
+    res, qkv = res0.clone(), qkv0.clone()
+
+    def chain():
+        ops.embedding_gather_q8(ids, tqd, tsd, out=emb)
+        ops.fused_add_rmsnorm(res, add, w, eps=1e-6, out=normed)
+        q = qkv[:, :NQ * HD].view(T, NQ, HD)
+        k = qkv[:, NQ * HD:(NQ + NKV) * HD].view(T, NKV, HD)
+        ops.qk_rmsnorm_rope(q, k, qw, kw, ct, st, positions=pos, eps=1e-6)
+        ops.swiglu_q8(gate, up, gs=32, out_q=codes, out_s=scales)
+
+    def snapshot():
+        torch.cuda.synchronize()
+        return [t.cpu().numpy().copy() for t in (emb, res, normed, qkv, codes, scales)]
+
+    chain()
+    want = snapshot()
+    res.copy_(res0)
+    qkv.copy_(qkv0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        chain()  # warm-up on the capture stream, as torch recommends
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        chain()
+    for replay in range(3):
+        for t in (emb, normed, codes, scales):
+            t.zero_()
+        res.copy_(res0)
+        qkv.copy_(qkv0)
+        torch.cuda.synchronize()
+        g.replay()
+        got = snapshot()
+        for name, a, b in zip(("emb", "residual", "normed", "qkv", "codes", "scales"), got, want):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (replay, name)
