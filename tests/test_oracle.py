@@ -231,6 +231,30 @@ def test_sigmoid_constants_and_special_values(oracle):
     assert float(oracle.sigmoid(float("nan"))) == 1.0
 
 
+def test_sigmoid_exact_where_the_exponent_is_an_integer(oracle):
+    """Inputs g whose fx = RN(-g * log2e) is an integer k leave f = fx - rint(fx) = 0, so the Horner
+    polynomial is exactly 1 (every term vanishes) and e = 2^k exactly: the reference's result is then
+    RN(1 / RN(1 + 2^k)), a closed form.  This pins the steps around the polynomial bit for bit: the
+    negation, the exponent built from k, the 1 + e and the final reciprocal (a swapped sign or e/(1+e)
+    for 1/(1+e) fails here; floor for rint, a contracted fx - rint(fx) or a misplaced coefficient fail
+    the dense sweep below)."""
+    log2e = F(1.4426950408889634)
+    checked = 0
+    for k in range(-23, 24):
+        y = F(k / 1.4426950408889634)
+        for _ in range(8):  # nearest float32 y with RN(y * log2e) == k
+            if F(y * log2e) == F(k):
+                break
+            y = np.nextafter(y, F(np.inf) if F(y * log2e) < k else F(-np.inf), dtype=F)
+        if F(y * log2e) != F(k):
+            continue
+        g = float(-y)
+        want = F(1.0) / (F(1.0) + F(2.0 ** k))  # 1 + 2^k is exact for |k| <= 23
+        assert bits_equal(np.array([oracle.sigmoid(g)], F), np.array([want], F)), (k, g)
+        checked += 1
+    assert checked >= 40
+
+
 def test_sigmoid_dense_sweep_vs_double(oracle):
     """The degree-5 exp2 polynomial is stated at 1.27e-7 max relative error (src/asm/v7_macros.inc:127-128).
     With the roundings around it the sigmoid stays within 5e-7 relative of double, plus the error that the
