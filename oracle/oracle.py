@@ -20,7 +20,9 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# V7G_ORACLE_LIB points the tests at another build of the same sources: the mutation check
+# (tests/test_oracle_mutations.py) builds copies with one planted mistake each.
+_LIB_PATH = os.environ.get("V7G_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")

@@ -80,6 +80,39 @@ def test_sumsq_leftover_blocks_first_known_answer(oracle):
     assert float(oracle.sumsq_lanes(x)) == TWO24 + 2
 
 
+def test_sumsq_hadd_pairing_known_answer(oracle):
+    """dim 32 with only block 0 non-zero, so the HADD_YMM input is v = x[0:8]^2 = [0, 9, 0, 2^24, 16, 9, 1, 9]:
+      s0 = v0 + v4 = 16, s1 = v1 + v5 = 18, s2 = v2 + v6 = 1, s3 = v3 + v7 = 2^24 + 9 -> 2^24 + 8 (tie to even),
+      t0 = s0 + s1 = 34, t2 = s2 + s3 = 2^24 + 9 -> 2^24 + 8, t0 + t2 = 2^24 + 42.
+    Pairing adjacent lanes, summing left to right, (s0 + s2) + (s1 + s3) or a sequential sum all give
+    2^24 + 40, 2^24 + 44 or similar instead."""
+    x = np.zeros(32, F)
+    x[:8] = [0, 3, 0, 4096, 4, 3, 1, 3]
+    assert float(oracle.sumsq_lanes(x)) == TWO24 + 42
+
+
+def test_sumsq_chains_are_fused_known_answer(oracle):
+    """dim 64: lane 0 of accumulator A takes x[0] = 2 then x[32] = 1 + 2^-23 (blocks 0 and 4).  With FMA the
+    chain is RN(4 + (1 + 2^-22 + 2^-46)) = 5 + 2^-21 (more than half an ulp above 5); a separate multiply
+    drops the 2^-46 first and the tie 5 + 2^-22 rounds to 5."""
+    x = np.zeros(64, F)
+    x[0] = 2.0
+    x[32] = F(1.0) + F(2.0 ** -23)
+    assert float(oracle.sumsq_lanes(x)) == 5.0 + 2.0 ** -21
+
+
+def test_rms_scale_step_roundings_known_answers(oracle):
+    """COMPUTE_RMS_SCALE rounds after each of vdivss, vaddss, vsqrtss, vdivss:
+      * sumsq/dim by division: sumsq = 24 + 2^-18, dim 24: 1 + 2^-23 (times RN(1/24) would give 1 + 2^-22),
+        whose square root lies below the midpoint 1 + 2^-24 and rounds to 1, so the scale is exactly 1
+        (1 + 2^-22 would give 1 - 2^-23);
+      * 1/sqrt in two roundings: mean v = 1.0000044107437134 gives RN(1/RN(sqrt v)) = 0.9999978542327881,
+        where the correctly rounded 1/sqrt(v) is 0.9999977946281433."""
+    assert float(oracle.rms_scale(F(24.0) + F(2.0 ** -18), 24, 0.0)) == 1.0
+    v = F(1.0000044107437134)
+    assert float(oracle.rms_scale(F(v * F(64)), 64, 0.0)) == float(F(0.9999978542327881))
+
+
 def test_rms_scale_closed_form(oracle):
     """COMPUTE_RMS_SCALE = 1/sqrt(sumsq/n + eps) in four correctly rounded steps: exact for powers of two."""
     assert float(oracle.rms_scale(F(4 * 64), 64, 0.0)) == 0.5
@@ -167,6 +200,49 @@ def test_rope_quarter_turn_and_identity_tables(oracle):
     s0 = np.zeros((2, half), F)
     got = oracle.rmsnorm_rope(x, w, c0, s0, np.ones(T, np.int32), 1e-6)
     assert bits_equal(got, n)
+
+
+def _rn32_exact(v):
+    """binary32 nearest-even of a float64 value that holds the exact result."""
+    return F(v)
+
+
+def test_rope_rotation_fused_known_answers(oracle):
+    """A head of ones with eps 0 has scale exactly 1, so xe = w_j and xo = w_{j+h} exactly.  With 16-bit
+    significands for w and the pos-1 table row, every product is exact in double, so the reference's
+    out_j = fma(-xo, sin, RN(xe*cos)) and out_{j+h} = fma(xo, cos, RN(xe*sin)) have closed forms with one
+    rounding each.  Unfused rotations, or the FMA on the other product, differ on part of the pairs."""
+    D, half = 64, 32
+    r = np.random.default_rng(77)
+    def v16(n):
+        return (r.integers(1 << 15, 1 << 16, n).astype(np.float64) / (1 << 15) * r.choice([-1.0, 1.0], n)).astype(F)
+    a, b, c1, s1 = v16(half), v16(half), v16(half), v16(half)
+    w = np.concatenate([a, b])
+    ct = np.stack([np.ones(half, F), c1])
+    st = np.stack([np.zeros(half, F), s1])
+    x = np.ones((1, 1, D), F)
+    got = oracle.rmsnorm_rope(x, w, ct, st, np.array([1], np.int32), 0.0)[0, 0]
+    a64, b64, c64, s64 = (t.astype(np.float64) for t in (a, b, c1, s1))
+    re = (a * c1).astype(F).astype(np.float64)  # RN(xe*cos)
+    ro = (a * s1).astype(F).astype(np.float64)  # RN(xe*sin)
+    want_lo = _rn32_exact(re - b64 * s64)
+    want_hi = _rn32_exact(ro + b64 * c64)
+    assert bits_equal(got[:half], want_lo) and bits_equal(got[half:], want_hi)
+    unfused = (re.astype(F) - (b * s1).astype(F)).astype(F)
+    other = _rn32_exact((-(b * s1)).astype(F).astype(np.float64) + a64 * c64)
+    assert not bits_equal(unfused, want_lo) and not bits_equal(other, want_lo)
+
+
+def test_rope_pos0_skips_the_tables(oracle):
+    """pos 0 takes the norm-only path whatever the table row 0 holds (here a quarter turn), for RMSNorm+RoPE
+    and for RoPE only (which returns the head unchanged)."""
+    x = C.normal(9, (1, 3, 64))
+    w = C.norm_weight(10, 64)
+    ct = np.zeros((1, 32), F)
+    st = np.ones((1, 32), F)
+    got = oracle.rmsnorm_rope(x, w, ct, st, np.zeros(1, np.int32), 1e-6)
+    assert bits_equal(got, _normed(oracle, x, w, 1e-6))
+    assert bits_equal(oracle.rope_only(x, ct, st, np.zeros(1, np.int32)), x)
 
 
 def test_rope_rotation_preserves_pair_norms(oracle):
@@ -337,6 +413,28 @@ def test_quantize_tail_group(oracle):
     assert bits_equal(q[0], kq)
 
 
+def test_quantize_ties_to_even_and_nan_codes(oracle):
+    """A group whose absmax is 127 has scale exactly 1 and reciprocal 1, so its codes are the nearest-even
+    integers of the inputs: vcvtps2dq on full groups and the tail's vcvtss2si both round ties to even
+    (2.5 -> 2, -3.5 -> -4, 0.5 -> 0, 126.5 -> 126).  A NaN element becomes -128 after the saturating packs
+    and -127 after vpmaxsb (full group), or -127 from the tail's vmaxss; a separately rounded tail or a
+    code left at -128 fails here."""
+    vals = np.array([127.0, 2.5, -3.5, 0.5, -0.5, 126.5], F)
+    want = np.array([127, 2, -4, 0, 0, 126], np.int8)
+    x = np.zeros(70, F)  # one full group of 64, then a 6-element tail
+    x[:6] = vals
+    x[64:] = vals
+    q, sc = oracle.quantize(x[None], 64)
+    assert sc[0, 0] == 1.0 and sc[0, 1] == 1.0
+    assert bits_equal(q[0, :6], want) and bits_equal(q[0, 64:], want) and not q[0, 6:64].any()
+    y = x.copy()
+    y[0] = np.nan  # absmax of the rest is still 127 (the NaN lane drops out of the max tree first)
+    y[1] = 127.0
+    y[64 + 5] = np.nan
+    q, _ = oracle.quantize(y[None], 64)
+    assert q[0, 0] == -127 and q[0, 64 + 5] == -127
+
+
 def test_swiglu_q8_is_quantize_of_swiglu_and_near_double(oracle):
     g = C.normal(401, (16, 8192), 1.5)
     u = C.normal(402, (16, 8192), 1.5)
@@ -502,6 +600,26 @@ def test_rope_only_known_answers(oracle):
     u = np.where(C.normal(2, (T, H, D)) > 0, 1.0, -1.0).astype(F)
     pos = np.array([1, 5, 7], np.int32)
     assert bits_equal(oracle.rope_only(u, ct, st, pos), oracle.rmsnorm_rope(u, np.ones(D, F), ct, st, pos, 0.0))
+
+
+def test_rope_only_fused_known_answers(oracle):
+    """With 16-bit significands for the head and the pos-1 table row every product is exact in double:
+    out_j = fma(-up, sin, RN(lo*cos)) and out_{j+h} = fma(up, cos, RN(lo*sin)) each round once."""
+    D, half = 64, 32
+    r = np.random.default_rng(78)
+    def v16(n):
+        return (r.integers(1 << 15, 1 << 16, n).astype(np.float64) / (1 << 15) * r.choice([-1.0, 1.0], n)).astype(F)
+    lo, up, c1, s1 = v16(half), v16(half), v16(half), v16(half)
+    x = np.concatenate([lo, up])[None, None, :]
+    ct = np.stack([np.ones(half, F), c1])
+    st = np.stack([np.zeros(half, F), s1])
+    got = oracle.rope_only(x, ct, st, np.array([1], np.int32))[0, 0]
+    re = (lo * c1).astype(F).astype(np.float64)
+    ro = (lo * s1).astype(F).astype(np.float64)
+    want_lo = F(re - up.astype(np.float64) * s1.astype(np.float64))
+    want_hi = F(ro + up.astype(np.float64) * c1.astype(np.float64))
+    assert bits_equal(got[:half], want_lo) and bits_equal(got[half:], want_hi)
+    assert not bits_equal((re.astype(F) - (up * s1).astype(F)).astype(F), want_lo)
 
 
 def test_rope_only_vs_double(oracle):
