@@ -182,6 +182,18 @@ int v7g_rope_init(int head_dim, float rope_base, int n_pos);
 /* Fills caller-owned device tables [n_pos, head_dim/2] (host-built in extended
  * precision, then copied; synchronous). */
 int v7g_build_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base);
+/* The same with Llama 3 frequency scaling: rope_build_internal_tables with
+ * rope type 1, src/asm/fused_f32_kernel.inc:149-256, whose parameters the
+ * reference reads from the model DB keys __sys_rope_factor,
+ * __sys_rope_low_freq_factor, __sys_rope_high_freq_factor and
+ * __sys_rope_orig_max_pos (:49-64).  factor > 0, 0 < low_freq_factor <
+ * high_freq_factor, orig_max_pos > 0. */
+int v7g_build_rope_tables_llama3(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base,
+                                 float factor, float low_freq_factor, float high_freq_factor, int orig_max_pos);
+/* Library-owned tables with Llama 3 frequency scaling (v7s_rope_init for a
+ * model whose rope type is 1); v7g_get_rope_tables returns them. */
+int v7g_rope_init_llama3(int head_dim, float rope_base, int n_pos, float factor, float low_freq_factor,
+                         float high_freq_factor, int orig_max_pos);
 
 /* Exhaustive self-check, on the current device, of the arithmetic identities
  * the kernels rely on: mismatches[0] = inputs d in [2^-126, 2^123) where rcp

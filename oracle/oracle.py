@@ -46,6 +46,10 @@ def lib():
             "orc_rmsnorm_rope_tokens": (None, [_f32p, c_int, c_ll, c_int, c_int, _f32p, _f32p, _f32p, _i32p, c_int,
                                                c_float]),
             "orc_rope_tables": (None, [_f32p, _f32p, c_int, c_int, c_float]),
+            "orc_rope_freqs_llama3": (None, [np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS"), c_int,
+                                             c_float, c_float, c_float, c_float, c_int]),
+            "orc_rope_tables_llama3": (None, [_f32p, _f32p, c_int, c_int, c_float, c_float, c_float, c_float,
+                                              c_int]),
             "orc_sigmoid": (c_float, [c_float]),
             "orc_swiglu": (None, [_f32p, _f32p, _f32p, c_ll]),
             "orc_quantize_rows": (None, [_i8p, _f32p, _f32p, c_int, c_int, c_int]),
@@ -117,6 +121,21 @@ def rope_tables(n_pos, head_dim, base):
     c = np.empty((n_pos, half), np.float32)
     s = np.empty((n_pos, half), np.float32)
     lib().orc_rope_tables(c, s, n_pos, head_dim, float(base))
+    return c, s
+
+
+def rope_freqs_llama3(half, base, factor, low_freq_factor, high_freq_factor, orig_max_pos):
+    """Llama 3 scaled RoPE frequencies (double), src/asm/fused_f32_kernel.inc:149-256."""
+    f = np.empty(half, np.float64)
+    lib().orc_rope_freqs_llama3(f, half, base, factor, low_freq_factor, high_freq_factor, orig_max_pos)
+    return f
+
+
+def rope_tables_llama3(n_pos, head_dim, base, factor, low_freq_factor, high_freq_factor, orig_max_pos):
+    half = head_dim // 2
+    c = np.empty((n_pos, half), np.float32)
+    s = np.empty((n_pos, half), np.float32)
+    lib().orc_rope_tables_llama3(c, s, n_pos, head_dim, base, factor, low_freq_factor, high_freq_factor, orig_max_pos)
     return c, s
 
 

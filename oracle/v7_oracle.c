@@ -183,6 +183,59 @@ void orc_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim
     }
 }
 
+/* RoPE frequencies with Llama 3 scaling (rope type 1):
+ * src/asm/fused_f32_kernel.inc:149-256 (.rbit_llama3_setup, .rbit_prefreq),
+ * the HF llama3 formula evaluated in x87 extended precision with the stores to
+ * double of the reference:
+ *   low_wl = old/low, high_wl = old/high                       (stored double)
+ *   inv = base^(-j/half)       (extended; stored double, the extended value
+ *                               goes on into the wavelength)
+ *   wavelen = 2 pi / inv                                       (stored double)
+ *   ifl = wavelen > low_wl ? inv/factor : inv                  (stored double)
+ *   smooth = (old/wavelen - low) / (high - low)                (stored double)
+ *   smoothed = (1 - smooth) * (ifl/factor) + smooth * ifl      (stored double)
+ *   freq = high_wl <= wavelen <= low_wl ? smoothed : ifl. */
+void orc_rope_freqs_llama3(double *freq, int half, float base, float factor, float low_freq_factor,
+                           float high_freq_factor, int orig_max_pos)
+{
+    const double two_pi = 6.28318530717958647692; /* rbit_two_pi */
+    const long double f = (double)factor, lo = (double)low_freq_factor, hi = (double)high_freq_factor;
+    const long double old = (double)orig_max_pos;
+    const double low_wl = (double)(old / lo);
+    const double high_wl = (double)(old / hi);
+    for (int j = 0; j < half; ++j) {
+        long double inv_x = powl((long double)base, -(long double)j / (long double)half);
+        double inv = (double)inv_x;
+        double wavelen = (double)((long double)two_pi / inv_x);
+        double ifl = (wavelen > low_wl) ? (double)((long double)inv / f) : inv;
+        double smooth = (double)((old / (long double)wavelen - lo) / (hi - lo));
+        double smoothed = (double)((1.0L - (long double)smooth) * ((long double)ifl / f) +
+                                   (long double)smooth * (long double)ifl);
+        int medium = wavelen >= high_wl && wavelen <= low_wl;
+        freq[j] = medium ? smoothed : ifl;
+    }
+}
+
+/* Tables from precomputed frequencies (the .rbit_outer / .rbit_inner fill, :257-303). */
+static void rope_fill(float *cos_table, float *sin_table, int n_pos, int half, const double *freq)
+{
+    for (int p = 0; p < n_pos; ++p)
+        for (int j = 0; j < half; ++j) {
+            long double a = (long double)freq[j] * (long double)p;
+            cos_table[(long long)p * half + j] = (float)cosl(a);
+            sin_table[(long long)p * half + j] = (float)sinl(a);
+        }
+}
+
+void orc_rope_tables_llama3(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base,
+                            float factor, float low_freq_factor, float high_freq_factor, int orig_max_pos)
+{
+    double freq[512];
+    int half = head_dim / 2;
+    orc_rope_freqs_llama3(freq, half, rope_base, factor, low_freq_factor, high_freq_factor, orig_max_pos);
+    rope_fill(cos_table, sin_table, n_pos, half, freq);
+}
+
 /* EVAL_SIGMOID, packed form: src/asm/v7_macros.inc:98-160; constants
  * src/asm/math_data.inc:16-53. */
 static float bits_to_float(uint32_t u)

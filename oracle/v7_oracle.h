@@ -38,6 +38,10 @@ void orc_rmsnorm_rope_tokens(float *buf, int n_tokens, long long token_stride, i
 
 /* a4: RoPE table builder (host, extended precision); tables are [n_pos, half] */
 void orc_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base);
+void orc_rope_freqs_llama3(double *freq, int half, float base, float factor, float low_freq_factor,
+                           float high_freq_factor, int orig_max_pos);
+void orc_rope_tables_llama3(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base,
+                            float factor, float low_freq_factor, float high_freq_factor, int orig_max_pos);
 
 /* a5: EVAL_SIGMOID, ps form */
 float orc_sigmoid(float g);

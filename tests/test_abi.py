@@ -142,6 +142,17 @@ def test_quantize_and_swiglu_reject(L):
     assert _sticky(L, L.v7g_swiglu_f32, None, None, None, 0) == (0, 0)
 
 
+def test_rope_table_builders_reject(L):
+    f = ctypes.c_float
+    assert _sticky(L, L.v7g_build_rope_tables_llama3, None, FAKE, 16, 128, f(5e5), f(8), f(1), f(4), 8192)[0] == 1
+    assert _sticky(L, L.v7g_build_rope_tables_llama3, FAKE, FAKE, 16, 128, f(5e5), f(0), f(1), f(4), 8192)[0] == 2
+    assert _sticky(L, L.v7g_build_rope_tables_llama3, FAKE, FAKE, 16, 128, f(5e5), f(8), f(4), f(4), 8192)[0] == 2
+    assert _sticky(L, L.v7g_build_rope_tables_llama3, FAKE, FAKE, 16, 128, f(5e5), f(8), f(1), f(4), 0)[0] == 2
+    assert _sticky(L, L.v7g_build_rope_tables_llama3, FAKE, FAKE, 0, 128, f(5e5), f(8), f(1), f(4), 8192)[0] == 2
+    assert _sticky(L, L.v7g_rope_init_llama3, 127, f(5e5), 16, f(8), f(1), f(4), 8192)[0] == 2
+    assert _sticky(L, L.v7g_rope_init_llama3, 128, f(5e5), 16, f(8), f(1), f(0.5), 8192)[0] == 2
+
+
 def test_embedding_rejects(L):
     assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE, FAKE, 100, 1000)[0] == 2  # dim % 64
     assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE, FAKE, 128, 0)[0] == 2

@@ -646,3 +646,38 @@ def test_chain_captured_in_a_hip_graph(ops, oracle):
         got = snapshot()
         for name, a, b in zip(("emb", "residual", "normed", "qkv", "codes", "scales"), got, want):
             assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (replay, name)
+
+
+def test_rope_tables_llama3_match_oracle(ops, oracle):
+    """Llama 3 scaled tables built by the library (host, extended precision) equal the oracle's bit for bit,
+    through the caller-owned builder and the library-owned v7g_rope_init_llama3; a RMSNorm+RoPE pass over them
+    is bit-exact too."""
+    import ctypes
+
+    from v7multiplikator_amd import _lib
+    p = dict(factor=8.0, low_freq_factor=1.0, high_freq_factor=4.0, original_max_position_embeddings=8192)
+    P, D, base = 4096, 128, 500000.0
+    wc, ws = oracle.rope_tables_llama3(P, D, base, 8.0, 1.0, 4.0, 8192)
+    c, s = ops.rope_tables(P, D, base, llama3=p)
+    assert_bits(host(c), wc, "cos")
+    assert_bits(host(s), ws, "sin")
+    L = _lib.load()
+    assert L.v7g_rope_init_llama3(D, ctypes.c_float(base), P, ctypes.c_float(8.0), ctypes.c_float(1.0),
+                                  ctypes.c_float(4.0), 8192) == 0
+    cp, sp, rmd, npos = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int(), ctypes.c_int()
+    assert L.v7g_get_rope_tables(ctypes.byref(cp), ctypes.byref(sp), ctypes.byref(rmd), ctypes.byref(npos)) == 0
+    assert rmd.value == D // 2 and npos.value == P
+    tc = torch.empty((P, D // 2), device="cuda")
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(tc.data_ptr(), cp.value, tc.numel() * 4, 3) == 0  # hipMemcpyDeviceToDevice
+    assert_bits(host(tc), wc, "owned cos")
+    T, H = 64, 8
+    buf = C.normal(8201, (T, H, D))
+    w = C.norm_weight(8202, D)
+    pos = C.rng(8203).integers(0, P, T).astype(np.int32)
+    bt = dev(buf)
+    ops.rmsnorm_rope_heads(bt, dev(w), c, s, positions=dev(pos), eps=1e-6)
+    assert_bits(host(bt), oracle.rmsnorm_rope(buf, w, wc, ws, pos, 1e-6), "rope over llama3 tables")
+    # restore the plain library-owned tables the drop-in test expects to be replaceable
+    assert L.v7g_rope_init(D, ctypes.c_float(1e6), 16) == 0

@@ -296,6 +296,59 @@ def test_rope_tables_vs_double(oracle):
     assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
 
 
+LLAMA31 = dict(base=500000.0, factor=8.0, low=1.0, high=4.0, orig=8192)  # Llama 3.1 8B config.json
+
+
+def test_rope_llama3_freqs_vs_transformers(oracle):
+    """The scaled frequencies equal the library routine transformers.modeling_rope_utils._compute_llama3_parameters
+    (torch float32) within its float32 rounding, for the Llama 3.1 8B parameters and for another set."""
+    pytest.importorskip("transformers")
+    from transformers import LlamaConfig
+    from transformers.modeling_rope_utils import _compute_llama3_parameters
+
+    for base, factor, low, high, orig, hd in ((500000.0, 8.0, 1.0, 4.0, 8192, 128), (10000.0, 4.0, 2.0, 8.0, 2048, 64)):
+        cfg = LlamaConfig(hidden_size=hd * 8, num_attention_heads=8, max_position_embeddings=4 * orig,
+                          rope_parameters={"rope_type": "llama3", "rope_theta": base, "factor": factor,
+                                           "low_freq_factor": low, "high_freq_factor": high,
+                                           "original_max_position_embeddings": orig})
+        inv, _ = _compute_llama3_parameters(cfg, device="cpu")
+        want = inv.double().numpy()
+        got = oracle.rope_freqs_llama3(hd // 2, base, factor, low, high, orig)
+        assert np.max(np.abs(got - want) / want) < 2e-6
+
+
+def test_rope_llama3_regimes_closed_forms(oracle):
+    """High frequencies (wavelength below orig/high) keep base^(-j/half); low frequencies (wavelength above
+    orig/low) are divided by factor; the band between interpolates, so it lies between the two; factor 1 is
+    the plain table."""
+    p = LLAMA31
+    half = 64
+    plain = np.power(np.float64(p["base"]), -np.arange(half, dtype=np.float64) / half)
+    got = oracle.rope_freqs_llama3(half, p["base"], p["factor"], p["low"], p["high"], p["orig"])
+    wl = 2 * np.pi / plain
+    hi_f, lo_f = wl < p["orig"] / p["high"], wl > p["orig"] / p["low"]
+    mid = ~hi_f & ~lo_f
+    assert hi_f.any() and lo_f.any() and mid.any()
+    assert np.allclose(got[hi_f], plain[hi_f], rtol=4e-16, atol=0)
+    assert np.allclose(got[lo_f], plain[lo_f] / p["factor"], rtol=4e-16, atol=0)
+    assert np.all(got[mid] <= plain[mid] * (1 + 1e-15)) and np.all(got[mid] >= plain[mid] / p["factor"] * (1 - 1e-15))
+    assert np.all(np.diff(got) < 0)  # still strictly decreasing in j
+    same = oracle.rope_freqs_llama3(half, p["base"], 1.0, p["low"], p["high"], p["orig"])
+    assert np.allclose(same, plain, rtol=4e-16, atol=0)
+
+
+def test_rope_llama3_tables_vs_double(oracle):
+    """cos/sin(pos * freq_j) rounded once to binary32: within 1 ulp of numpy double on the scaled frequencies."""
+    p = LLAMA31
+    P, D = 1024, 128
+    c, s = oracle.rope_tables_llama3(P, D, p["base"], p["factor"], p["low"], p["high"], p["orig"])
+    f = oracle.rope_freqs_llama3(D // 2, p["base"], p["factor"], p["low"], p["high"], p["orig"])
+    ang = np.arange(P, dtype=np.float64)[:, None] * f[None, :]
+    dc, ds = np.cos(ang), np.sin(ang)
+    assert np.all(np.abs(c - dc) <= np.spacing(np.abs(dc).astype(F)) + 1e-12)
+    assert np.all(np.abs(s - ds) <= np.spacing(np.abs(ds).astype(F)) + 1e-12)
+
+
 # --------------------------------------------------------------------------- sigmoid / SwiGLU (a5, a6, a8)
 
 def test_sigmoid_constants_and_special_values(oracle):

@@ -151,6 +151,17 @@ MUTANTS = [
     ("rope_only: no fma",
      "            re = fmaf(-up, s[j], re);",
      "            re = re - up * s[j];"),
+    ("llama3: divides the high band",
+     "        double ifl = (wavelen > low_wl) ? (double)((long double)inv / f) : inv;",
+     "        double ifl = (wavelen < low_wl) ? (double)((long double)inv / f) : inv;"),
+    ("llama3: interpolation weights swapped",
+     "        double smoothed = (double)((1.0L - (long double)smooth) * ((long double)ifl / f) +\n"
+     "                                   (long double)smooth * (long double)ifl);",
+     "        double smoothed = (double)((long double)smooth * ((long double)ifl / f) +\n"
+     "                                   (1.0L - (long double)smooth) * (long double)ifl);"),
+    ("llama3: no medium band",
+     "        int medium = wavelen >= high_wl && wavelen <= low_wl;",
+     "        int medium = wavelen >= low_wl && wavelen <= high_wl;"),
     ("rmsnorm: (s*w)*x",
      "        float t = s * x[i];\n"
      "        o[i] = t * weight[i];",

@@ -84,14 +84,47 @@ int check_rope_side(const float *buf, long long token_stride, int n_heads, int h
   return V7G_OK;
 }
 
-// Host RoPE table builder: src/asm/fused_f32_kernel.inc:69-147,257-303 (plain
-// rope type).  freq_j = base^(-j/half), computed in extended precision and
-// kept as a double as the reference stores it; angle = freq_j * pos in
-// extended precision; cos/sin rounded to float.
-void build_tables_host(std::vector<float> &c, std::vector<float> &s, int n_pos, int half, float base) {
+// Host RoPE table builder: src/asm/fused_f32_kernel.inc:69-303.  The
+// frequencies are computed in extended precision and kept as doubles, as the
+// reference's x87 code stores them; angle = freq_j * pos in extended
+// precision; cos/sin rounded to float.
+
+// Plain tables (rope type 0, :120-147): freq_j = base^(-j/half).
+std::vector<double> plain_freqs(int half, float base) {
   std::vector<double> freq(half);
   for (int j = 0; j < half; ++j)
     freq[j] = (double)std::pow((long double)base, -(long double)j / (long double)half);
+  return freq;
+}
+
+// Llama 3 frequency scaling (rope type 1, :149-256), the values rounded to
+// double where the reference stores them: wavelen_j = 2 pi / inv_j; below the
+// high-frequency wavelength inv_j is kept, above the low-frequency wavelength
+// it is divided by factor, and in between it is interpolated with
+// smooth = (orig/wavelen - low) / (high - low).
+std::vector<double> llama3_freqs(int half, float base, float factor, float low_freq_factor, float high_freq_factor,
+                                 int orig_max_pos) {
+  typedef long double X;
+  const double two_pi = 6.28318530717958647692;
+  const double f = factor, lo = low_freq_factor, hi = high_freq_factor, old = orig_max_pos;
+  const double low_wl = (double)((X)old / (X)lo);
+  const double high_wl = (double)((X)old / (X)hi);
+  std::vector<double> freq(half);
+  for (int j = 0; j < half; ++j) {
+    const X inv_x = std::pow((X)base, -(X)j / (X)half);
+    const double inv = (double)inv_x;
+    const double wavelen = (double)((X)two_pi / inv_x);
+    const double ifl = wavelen > low_wl ? (double)((X)inv / (X)f) : inv;
+    const double smooth = (double)(((X)old / (X)wavelen - (X)lo) / ((X)hi - (X)lo));
+    const double smoothed = (double)((1.0L - (X)smooth) * ((X)ifl / (X)f) + (X)smooth * (X)ifl);
+    const bool medium = wavelen >= high_wl && wavelen <= low_wl;
+    freq[j] = medium ? smoothed : ifl;
+  }
+  return freq;
+}
+
+void fill_tables(std::vector<float> &c, std::vector<float> &s, int n_pos, const std::vector<double> &freq) {
+  const int half = (int)freq.size();
   c.resize((size_t)n_pos * half);
   s.resize((size_t)n_pos * half);
   unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
@@ -107,6 +140,61 @@ void build_tables_host(std::vector<float> &c, std::vector<float> &s, int n_pos, 
     });
   }
   for (auto &t : th) t.join();
+}
+
+int check_table_shape(int n_pos, int head_dim) {
+  return (n_pos <= 0 || n_pos > kRopeMaxPositions || head_dim < 2 || head_dim % 2 != 0 || head_dim > 1024)
+             ? V7G_ERR_SHAPE
+             : V7G_OK;
+}
+
+int check_llama3(float factor, float low_freq_factor, float high_freq_factor, int orig_max_pos) {
+  const bool ok = factor > 0.0f && low_freq_factor > 0.0f && high_freq_factor > low_freq_factor &&
+                  orig_max_pos > 0 && std::isfinite(factor) && std::isfinite(high_freq_factor);
+  return ok ? V7G_OK : V7G_ERR_SHAPE;
+}
+
+int copy_tables(float *cos_table, float *sin_table, const std::vector<float> &c, const std::vector<float> &s) {
+  const size_t bytes = c.size() * sizeof(float);
+  if (hipMemcpy(cos_table, c.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) return V7G_ERR_HIP;
+  if (hipMemcpy(sin_table, s.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) return V7G_ERR_HIP;
+  return V7G_OK;
+}
+
+// Allocates library-owned tables from freq and publishes them, releasing the
+// previous ones (v7s_rope_init owns its tables, fused_dispatch.inc:58-76).
+int own_tables(int n_pos, const std::vector<double> &freq) {
+  std::lock_guard<std::mutex> lk(g_rope_mu);
+  if (g_rope_cos) {
+    // Launches already queued, on any host thread's stream, may still read
+    // the old tables: wait for the whole device before releasing them.
+    if (hipDeviceSynchronize() != hipSuccess) return V7G_ERR_HIP;
+    (void)hipFree(g_rope_cos);
+    (void)hipFree(g_rope_sin);
+    g_rope_cos = g_rope_sin = nullptr;
+    g_rope_half = g_rope_npos = 0;
+  }
+  const int half = (int)freq.size();
+  const size_t bytes = (size_t)n_pos * half * sizeof(float);
+  float *c = nullptr, *s = nullptr;
+  if (hipMalloc(&c, bytes) != hipSuccess) return V7G_ERR_HIP;
+  if (hipMalloc(&s, bytes) != hipSuccess) {
+    (void)hipFree(c);
+    return V7G_ERR_HIP;
+  }
+  std::vector<float> hc, hs;
+  fill_tables(hc, hs, n_pos, freq);
+  const int rc = copy_tables(c, s, hc, hs);
+  if (rc != V7G_OK) {
+    (void)hipFree(c);
+    (void)hipFree(s);
+    return rc;
+  }
+  g_rope_cos = c;
+  g_rope_sin = s;
+  g_rope_half = half;
+  g_rope_npos = n_pos;
+  return V7G_OK;
 }
 
 hipStream_t stream() { return g_stream; }
@@ -162,49 +250,38 @@ const char *v7g_error_string(int code) {
 
 int v7g_build_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base) {
   if (!cos_table || !sin_table) return fail(V7G_ERR_NULL);
-  if (n_pos <= 0 || n_pos > kRopeMaxPositions || head_dim < 2 || head_dim % 2 != 0 || head_dim > 1024)
-    return fail(V7G_ERR_SHAPE);
+  if (int rc = check_table_shape(n_pos, head_dim)) return fail(rc);
   std::vector<float> c, s;
-  int half = head_dim / 2;
-  build_tables_host(c, s, n_pos, half, rope_base);
-  size_t bytes = c.size() * sizeof(float);
-  if (hipMemcpy(cos_table, c.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) return fail(V7G_ERR_HIP);
-  if (hipMemcpy(sin_table, s.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) return fail(V7G_ERR_HIP);
-  return V7G_OK;
+  fill_tables(c, s, n_pos, plain_freqs(head_dim / 2, rope_base));
+  const int rc = copy_tables(cos_table, sin_table, c, s);
+  return rc ? fail(rc) : V7G_OK;
+}
+
+int v7g_build_rope_tables_llama3(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base,
+                                 float factor, float low_freq_factor, float high_freq_factor, int orig_max_pos) {
+  if (!cos_table || !sin_table) return fail(V7G_ERR_NULL);
+  if (int rc = check_table_shape(n_pos, head_dim)) return fail(rc);
+  if (int rc = check_llama3(factor, low_freq_factor, high_freq_factor, orig_max_pos)) return fail(rc);
+  std::vector<float> c, s;
+  fill_tables(c, s, n_pos,
+              llama3_freqs(head_dim / 2, rope_base, factor, low_freq_factor, high_freq_factor, orig_max_pos));
+  const int rc = copy_tables(cos_table, sin_table, c, s);
+  return rc ? fail(rc) : V7G_OK;
 }
 
 int v7g_rope_init(int head_dim, float rope_base, int n_pos) {
-  if (n_pos <= 0 || n_pos > kRopeMaxPositions || head_dim < 2 || head_dim % 2 != 0 || head_dim > 1024)
-    return fail(V7G_ERR_SHAPE);
-  std::lock_guard<std::mutex> lk(g_rope_mu);
-  if (g_rope_cos) {
-    // Launches already queued, on any host thread's stream, may still read
-    // the old tables: wait for the whole device before releasing them.
-    if (hipDeviceSynchronize() != hipSuccess) return fail(V7G_ERR_HIP);
-    (void)hipFree(g_rope_cos);
-    (void)hipFree(g_rope_sin);
-    g_rope_cos = g_rope_sin = nullptr;
-    g_rope_half = g_rope_npos = 0;
-  }
-  int half = head_dim / 2;
-  size_t bytes = (size_t)n_pos * half * sizeof(float);
-  float *c = nullptr, *s = nullptr;
-  if (hipMalloc(&c, bytes) != hipSuccess) return fail(V7G_ERR_HIP);
-  if (hipMalloc(&s, bytes) != hipSuccess) {
-    (void)hipFree(c);
-    return fail(V7G_ERR_HIP);
-  }
-  int rc = v7g_build_rope_tables(c, s, n_pos, head_dim, rope_base);
-  if (rc != V7G_OK) {
-    (void)hipFree(c);
-    (void)hipFree(s);
-    return rc;
-  }
-  g_rope_cos = c;
-  g_rope_sin = s;
-  g_rope_half = half;
-  g_rope_npos = n_pos;
-  return V7G_OK;
+  if (int rc = check_table_shape(n_pos, head_dim)) return fail(rc);
+  const int rc = own_tables(n_pos, plain_freqs(head_dim / 2, rope_base));
+  return rc ? fail(rc) : V7G_OK;
+}
+
+int v7g_rope_init_llama3(int head_dim, float rope_base, int n_pos, float factor, float low_freq_factor,
+                         float high_freq_factor, int orig_max_pos) {
+  if (int rc = check_table_shape(n_pos, head_dim)) return fail(rc);
+  if (int rc = check_llama3(factor, low_freq_factor, high_freq_factor, orig_max_pos)) return fail(rc);
+  const int rc = own_tables(
+      n_pos, llama3_freqs(head_dim / 2, rope_base, factor, low_freq_factor, high_freq_factor, orig_max_pos));
+  return rc ? fail(rc) : V7G_OK;
 }
 
 int v7g_arith_selfcheck(unsigned long long *mismatches) {

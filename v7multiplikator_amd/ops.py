@@ -17,7 +17,8 @@ library the first call raises.
   quantize_q8        <- v7d_quantize            (src/asm/utility_dispatch.inc:108-212)
   swiglu_q8          <- SwiGLU then v7d_quantize (src/asm/prefill_q8.inc:1154-1183)
   embedding_gather_q8 <- v7s_embedding_row      (src/asm/forward.inc:13-42)
-  rope_tables        <- v7s_rope_init           (src/asm/fused_dispatch.inc:58-76)
+  rope_tables        <- v7s_rope_init           (src/asm/fused_dispatch.inc:58-76; Llama 3 scaling
+                                                  src/asm/fused_f32_kernel.inc:149-256)
   kv_pack_f16        <- v7s_kv_pack_f16         (src/asm/kv_f16c.inc:12-52)
   rope_only_heads    <- v7s_rope_only_heads     (src/asm/rope_only_dispatch.inc:11-47)
   qkv_rope_stage     <- the per-token Q/K/V stage of the prefill, one launch (src/asm/prefill_q8.inc:848-883)
@@ -371,12 +372,22 @@ def kv_pack_f16(src: torch.Tensor, out: torch.Tensor | None = None) -> torch.Ten
     return out
 
 
-def rope_tables(n_pos: int, head_dim: int, rope_base: float, device="cuda"):
-    """Device cos/sin tables [n_pos, head_dim/2] (freq_j = base^(-j/half)), built on the host."""
+def rope_tables(n_pos: int, head_dim: int, rope_base: float, device="cuda", llama3: dict | None = None):
+    """Device cos/sin tables [n_pos, head_dim/2] (freq_j = base^(-j/half)), built on the host.
+
+    llama3: the Llama 3 frequency scaling (rope type 1), a dict with factor, low_freq_factor,
+    high_freq_factor and original_max_position_embeddings."""
     half = head_dim // 2
     c = torch.empty((n_pos, half), dtype=torch.float32, device=device)
     s = torch.empty((n_pos, half), dtype=torch.float32, device=device)
     torch.cuda.synchronize(c.device)
-    rc = _lib.load().v7g_build_rope_tables(c.data_ptr(), s.data_ptr(), n_pos, head_dim, float(rope_base))
+    L = _lib.load()
+    if llama3 is None:
+        rc = L.v7g_build_rope_tables(c.data_ptr(), s.data_ptr(), n_pos, head_dim, float(rope_base))
+    else:
+        rc = L.v7g_build_rope_tables_llama3(c.data_ptr(), s.data_ptr(), n_pos, head_dim, float(rope_base),
+                                            float(llama3["factor"]), float(llama3["low_freq_factor"]),
+                                            float(llama3["high_freq_factor"]),
+                                            int(llama3["original_max_position_embeddings"]))
     _lib.check(rc, "rope_tables")
     return c, s
