@@ -123,7 +123,9 @@ __device__ __forceinline__ uint2 pack4_f16(float4 v) {
 // Infinity Cache (MALL): the reused lines (RoPE tables, norm weights, table
 // scales) stay resident, and a kernel leaves no dirty lines behind for the
 // next kernel of the chain to write back.  Measured on MI355X over the whole
-// per-layer chain, every kernel is fastest with streaming loads and stores.
+// per-layer chain, every kernel is fastest with streaming loads and stores,
+// except that the embedding gather writes its output rows with ordinary
+// stores (they stay cached for the layer that reads them next).
 typedef float v7g_f4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 ld_stream4(const float *p) {
   v7g_f4 a = __builtin_nontemporal_load(reinterpret_cast<const v7g_f4 *>(p));
