@@ -37,6 +37,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "v7g_lib.h"
@@ -542,6 +543,14 @@ int main(int argc, char **argv) {
   hipStream_t st;
   HIPCHECK(hipStreamCreate(&st));
   L.set_stream(st);
+  {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    HIPCHECK(hipGetDevice(&dev));
+    HIPCHECK(hipGetDeviceProperties(&prop, dev));
+    printf("device %d: %s (%s), %d CUs; host cores %u\n", dev, prop.name, prop.gcnArchName, prop.multiProcessorCount,
+           std::thread::hardware_concurrency());
+  }
   auto num = [&](size_t i, int dflt) { return i < pos.size() ? atoi(pos[i].c_str()) : dflt; };
   const std::string k = pos[0];
   if (k == "fused_add_rmsnorm" && pos.size() >= 3)
