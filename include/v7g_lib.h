@@ -49,6 +49,7 @@ extern "C" {
 #define V7G_ERR_ALIGN 3      /* a pointer is not aligned as the kernel needs */
 #define V7G_ERR_HIP 4        /* the HIP runtime reported an error */
 #define V7G_ERR_NO_TABLES 5  /* RoPE tables requested before v7s_rope_init */
+#define V7G_ERR_ADDRESS 6    /* a pointer is not memory the current device can access (pointer checks on) */
 
 /* Q8 tensor descriptor: int8 codes + per-group f32 scales (GS = 64).
  * Same layout as v7_q8_tensor, src/v7_lib.h:52-56. */
@@ -167,6 +168,20 @@ int v7g_sync(void);
  * empty call) leaves the pair armed; a launching call disarms it.  Returns
  * V7G_OK. */
 int v7g_time_next_call(void *start_event, void *stop_event);
+/* Pointer checks (no counterpart in the reference, whose kernels read host
+ * memory).  When on, every entry asks the HIP runtime whether each pointer it
+ * was given is device memory of the current device, managed memory or pinned
+ * host memory, and rejects any other pointer with V7G_ERR_ADDRESS before
+ * launching: a host buffer handed to a drop-in entry by mistake becomes an
+ * error code instead of a GPU memory fault.  Off by default (each check costs
+ * a runtime query per pointer); the environment variable V7G_CHECK_POINTERS=1
+ * turns them on at load.  Process-wide. */
+void v7g_set_pointer_checks(int on);
+int v7g_get_pointer_checks(void);
+/* The same test for one pointer, whatever the switch says: V7G_OK if the
+ * current device can access p, else V7G_ERR_ADDRESS (not recorded as the
+ * sticky error). */
+int v7g_check_pointer(const void *p);
 /* eps used by the drop-in norm entries (the reference's g_rms_eps global,
  * src/asm/v7_data.inc:509; default 1e-6). */
 void v7g_set_rms_eps(float eps);

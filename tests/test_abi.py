@@ -142,6 +142,20 @@ def test_quantize_and_swiglu_reject(L):
     assert _sticky(L, L.v7g_swiglu_f32, None, None, None, 0) == (0, 0)
 
 
+def test_pointer_checks_switch_and_error_string(L):
+    """Pointer checks are off by default (no V7G_CHECK_POINTERS in the environment) and switch per process;
+    their error code has its own message.  The checks themselves need a device (tests/test_gpu_parity.py)."""
+    before = L.v7g_get_pointer_checks()
+    try:
+        L.v7g_set_pointer_checks(1)
+        assert L.v7g_get_pointer_checks() == 1
+        L.v7g_set_pointer_checks(0)
+        assert L.v7g_get_pointer_checks() == 0
+    finally:
+        L.v7g_set_pointer_checks(before)
+    assert L.v7g_error_string(6) == b"a pointer is not memory the current device can access"
+
+
 def test_rope_table_builders_reject(L):
     f = ctypes.c_float
     assert _sticky(L, L.v7g_build_rope_tables_llama3, None, FAKE, 16, 128, f(5e5), f(8), f(1), f(4), 8192)[0] == 1

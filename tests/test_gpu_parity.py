@@ -681,3 +681,34 @@ def test_rope_tables_llama3_match_oracle(ops, oracle):
     assert_bits(host(bt), oracle.rmsnorm_rope(buf, w, wc, ws, pos, 1e-6), "rope over llama3 tables")
     # restore the plain library-owned tables the drop-in test expects to be replaceable
     assert L.v7g_rope_init(D, ctypes.c_float(1e6), 16) == 0
+
+
+def test_pointer_checks_reject_host_memory(ops):
+    """With pointer checks on, a pageable host buffer is rejected with V7G_ERR_ADDRESS before any launch, while
+    device memory and pinned host memory pass; with checks off (the default) nothing is queried."""
+    from v7multiplikator_amd import _lib
+    L = _lib.load()
+    n = 4096
+    host_x = np.ones(n, np.float32)  # pageable host memory: the GPU must never see this pointer
+    dx = torch.ones(n, device="cuda")
+    dy = torch.ones(n, device="cuda")
+    pinned = torch.ones(n, dtype=torch.float32).pin_memory()
+    L.v7g_set_stream(torch.cuda.current_stream().cuda_stream)
+    # classify first, launching nothing: the entry below is only called with the host pointer once the
+    # runtime is known to report it as inaccessible
+    assert L.v7g_check_pointer(host_x.ctypes.data) == _lib.V7G_ERR_ADDRESS
+    assert L.v7g_check_pointer(dx.data_ptr()) == 0 and L.v7g_check_pointer(pinned.data_ptr()) == 0
+    try:
+        L.v7g_set_pointer_checks(1)
+        L.v7g_clear_last_error()
+        assert L.v7g_add_inplace(host_x.ctypes.data, dy.data_ptr(), n) == _lib.V7G_ERR_ADDRESS
+        assert L.v7g_get_last_error() == _lib.V7G_ERR_ADDRESS
+        L.v7g_clear_last_error()
+        assert L.v7g_add_inplace(dx.data_ptr(), dy.data_ptr(), n) == 0
+        assert L.v7g_add_inplace(dx.data_ptr(), pinned.data_ptr(), n) == 0
+        torch.cuda.synchronize()
+        assert torch.all(dx == 3.0).item()
+        assert L.v7g_get_last_error() == 0
+    finally:
+        L.v7g_set_pointer_checks(0)
+        L.v7g_clear_last_error()

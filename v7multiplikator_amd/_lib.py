@@ -17,6 +17,7 @@ V7G_ERR_SHAPE = 2
 V7G_ERR_ALIGN = 3
 V7G_ERR_HIP = 4
 V7G_ERR_NO_TABLES = 5
+V7G_ERR_ADDRESS = 6
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -32,6 +33,9 @@ SIGNATURES = {
     "v7g_get_stream": (_vp, []),
     "v7g_sync": (_i, []),
     "v7g_time_next_call": (_i, [_vp, _vp]),
+    "v7g_set_pointer_checks": (None, [_i]),
+    "v7g_get_pointer_checks": (_i, []),
+    "v7g_check_pointer": (_i, [_vp]),
     "v7g_set_rms_eps": (None, [_f]),
     "v7g_get_rms_eps": (_f, []),
     "v7g_get_last_error": (_i, []),

@@ -9,7 +9,9 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <cmath>
 #include <mutex>
 #include <thread>
@@ -50,6 +52,51 @@ int check_launch() {
 }
 
 bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Pointer checks: off unless V7G_CHECK_POINTERS=1 or v7g_set_pointer_checks(1).
+std::atomic<int> g_ptr_checks{-1};
+
+bool pointer_checks() {
+  int on = g_ptr_checks.load(std::memory_order_relaxed);
+  if (on < 0) {
+    const char *e = std::getenv("V7G_CHECK_POINTERS");
+    on = (e && e[0] == '1') ? 1 : 0;
+    int unset = -1;
+    g_ptr_checks.compare_exchange_strong(unset, on);
+    on = g_ptr_checks.load();
+  }
+  return on == 1;
+}
+
+// Device memory of the current device, managed memory or pinned host memory.
+bool device_accessible(const void *p) {
+  hipPointerAttribute_t a;
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();  // an unknown pointer is an answer here, not a pending error
+    return false;
+  }
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  switch (a.type) {
+    case hipMemoryTypeDevice:
+    case hipMemoryTypeArray:
+      return a.device == dev;
+    case hipMemoryTypeHost:
+    case hipMemoryTypeManaged:
+    case hipMemoryTypeUnified:
+      return true;
+    default:
+      return false;
+  }
+}
+
+// V7G_ERR_ADDRESS if pointer checks are on and a non-null pointer fails them.
+int check_ptrs(std::initializer_list<const void *> ps) {
+  if (!pointer_checks()) return V7G_OK;
+  for (const void *p : ps)
+    if (p && !device_accessible(p)) return V7G_ERR_ADDRESS;
+  return V7G_OK;
+}
 
 int check_add_rmsnorm(const float *o, const float *residual, const float *add, const float *weight, int rows, int dim) {
   if (rows < 0 || dim <= 0 || dim % 8 != 0 || dim > kMaxNormDim) return V7G_ERR_SHAPE;
@@ -219,6 +266,10 @@ int v7g_init(void) {
   return V7G_OK;
 }
 
+void v7g_set_pointer_checks(int on) { g_ptr_checks.store(on ? 1 : 0); }
+int v7g_get_pointer_checks(void) { return pointer_checks() ? 1 : 0; }
+int v7g_check_pointer(const void *p) { return (p && device_accessible(p)) ? V7G_OK : V7G_ERR_ADDRESS; }
+
 void v7g_set_stream(void *s) { g_stream = reinterpret_cast<hipStream_t>(s); }
 void *v7g_get_stream(void) { return reinterpret_cast<void *>(g_stream); }
 
@@ -244,6 +295,7 @@ const char *v7g_error_string(int code) {
     case V7G_ERR_ALIGN: return "a pointer is not aligned as the kernel needs";
     case V7G_ERR_HIP: return "the HIP runtime reported an error";
     case V7G_ERR_NO_TABLES: return "RoPE tables requested before v7s_rope_init";
+    case V7G_ERR_ADDRESS: return "a pointer is not memory the current device can access";
     default: return "unknown error";
   }
 }
@@ -308,6 +360,7 @@ int v7g_fused_add_rmsnorm(float *o, float *residual, const float *add, const flo
   int rc = check_add_rmsnorm(o, residual, add, weight, rows, dim);
   if (rc) return fail(rc);
   if (rows == 0) return V7G_OK;
+  if (int pc = check_ptrs({o, residual, add, weight})) return fail(pc);
   v7g::launch_fused_add_rmsnorm(o, residual, add, weight, rows, dim, eps, stream());
   return check_launch();
 }
@@ -317,6 +370,7 @@ int v7g_rmsnorm(float *o, const float *x, const float *weight, int rows, int dim
   if (rows == 0) return V7G_OK;
   if (!o || !x || !weight) return fail(V7G_ERR_NULL);
   if (!al16(o) || !al16(x) || !al16(weight)) return fail(V7G_ERR_ALIGN);
+  if (int pc = check_ptrs({o, x, weight})) return fail(pc);
   v7g::launch_rmsnorm(o, x, weight, rows, dim, eps, stream());
   return check_launch();
 }
@@ -335,6 +389,7 @@ int v7g_rmsnorm_quantize(int8_t *out_q, float *out_s, const float *x, const floa
   int rc = check_norm_q8(out_q, out_s, x, weight, rows, dim, gs);
   if (rc) return fail(rc);
   if (rows == 0) return V7G_OK;
+  if (int pc = check_ptrs({out_q, out_s, x, weight})) return fail(pc);
   v7g::launch_rmsnorm_quantize(out_q, out_s, const_cast<float *>(x), nullptr, weight, rows, dim, gs, eps, stream());
   return check_launch();
 }
@@ -346,6 +401,7 @@ int v7g_add_rmsnorm_quantize(int8_t *out_q, float *out_s, float *residual, const
   if (!rc && rows > 0 && !al16(add)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (rows == 0) return V7G_OK;
+  if (int pc = check_ptrs({out_q, out_s, residual, add, weight})) return fail(pc);
   v7g::launch_rmsnorm_quantize(out_q, out_s, residual, add, weight, rows, dim, gs, eps, stream());
   return check_launch();
 }
@@ -355,6 +411,7 @@ int v7g_add_inplace(float *x, const float *y, long long n) {
   if (n == 0) return V7G_OK;
   if (!x || !y) return fail(V7G_ERR_NULL);
   if (!al16(x) || !al16(y)) return fail(V7G_ERR_ALIGN);
+  if (int pc = check_ptrs({x, y})) return fail(pc);
   v7g::launch_add_inplace(x, y, n, stream());
   return check_launch();
 }
@@ -368,6 +425,7 @@ int v7g_rmsnorm_rope_heads(float *buf, int n_tokens, long long token_stride, int
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
+  if (int pc = check_ptrs({buf, norm_weight, cos_table, sin_table, positions})) return fail(pc);
   v7g::RopeSide side{buf, token_stride, n_heads, norm_weight};
   v7g::launch_rmsnorm_rope(&side, 1, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
                            table_rows, eps, stream());
@@ -385,6 +443,7 @@ int v7g_qk_rmsnorm_rope(float *q, long long q_token_stride, int n_q_heads, const
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
+  if (int pc = check_ptrs({q, q_norm_weight, k, k_norm_weight, cos_table, sin_table, positions})) return fail(pc);
   v7g::RopeSide sides[2] = {{q, q_token_stride, n_q_heads, q_norm_weight},
                             {k, k_token_stride, n_kv_heads, k_norm_weight}};
   v7g::launch_rmsnorm_rope(sides, 2, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
@@ -441,6 +500,11 @@ int v7g_qkv_rope_stage(const v7g_qkv_stage *st) {
   if (!rc && st->positions && ((uintptr_t)st->positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (st->n_tokens == 0) return V7G_OK;
+  if (int pc = check_ptrs({st->q.buf, st->q.norm_weight, st->q.bias, st->k.buf, st->k.norm_weight, st->k.bias,
+                           st->k.cache, st->cos_table, st->sin_table, st->positions}))
+    return fail(pc);
+  if (has_v)
+    if (int pc = check_ptrs({st->v.buf, st->v.bias, st->v.cache})) return fail(pc);
   v7g::RopeSide sides[3];
   const v7g_qkv_side *src[3] = {&st->q, &st->k, &st->v};
   for (int i = 0; i < 3; ++i) {
@@ -475,6 +539,7 @@ int v7g_rope_only_heads(float *buf, int n_tokens, long long token_stride, int n_
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
+  if (int pc = check_ptrs({buf, cos_table, sin_table, positions})) return fail(pc);
   v7g::RopeSide side{buf, token_stride, n_heads, nullptr};
   v7g::launch_rmsnorm_rope(&side, 1, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
                            table_rows, 0.0f, stream());
@@ -490,6 +555,7 @@ int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long 
   if (rows == 0) return V7G_OK;
   if (!dst || !src) return fail(V7G_ERR_NULL);
   if (((uintptr_t)dst & 7u) || !al16(src)) return fail(V7G_ERR_ALIGN);
+  if (int pc = check_ptrs({dst, src})) return fail(pc);
   v7g::launch_kv_pack_f16(dst, dst_stride, src, src_stride, rows, row_len, stream());
   return check_launch();
 }
@@ -499,6 +565,7 @@ int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n) 
   if (n == 0) return V7G_OK;
   if (!out || !gate || !up) return fail(V7G_ERR_NULL);
   if (!al16(out) || !al16(gate) || !al16(up)) return fail(V7G_ERR_ALIGN);
+  if (int pc = check_ptrs({out, gate, up})) return fail(pc);
   v7g::launch_swiglu_f32(out, gate, up, n, stream());
   return check_launch();
 }
@@ -519,6 +586,7 @@ int v7g_swiglu_q8(int8_t *out_q, float *out_s, const float *gate, const float *u
   if (!rc && rows > 0 && (!gate || !up)) rc = V7G_ERR_NULL;
   if (rc) return fail(rc);
   if (rows == 0) return V7G_OK;
+  if (int pc = check_ptrs({out_q, out_s, gate, up})) return fail(pc);
   v7g::launch_quantize_q8(out_q, out_s, nullptr, gate, up, rows, hidden, gs, stream());
   return check_launch();
 }
@@ -528,6 +596,7 @@ int v7g_quantize_q8(int8_t *out_q, float *out_s, const float *x, int rows, int r
   if (!rc && rows > 0 && !x) rc = V7G_ERR_NULL;
   if (rc) return fail(rc);
   if (rows == 0) return V7G_OK;
+  if (int pc = check_ptrs({out_q, out_s, x})) return fail(pc);
   v7g::launch_quantize_q8(out_q, out_s, x, nullptr, nullptr, rows, row_len, gs, stream());
   return check_launch();
 }
@@ -541,6 +610,7 @@ int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const 
   if ((long long)n_tokens * ((dim / 4 + 1023) / 1024) >= (1LL << 24)) return fail(V7G_ERR_SHAPE);
   if (!al16(out) || ((uintptr_t)table_q & 3u) || ((uintptr_t)table_s & 3u) || ((uintptr_t)ids & 3u))
     return fail(V7G_ERR_ALIGN);
+  if (int pc = check_ptrs({out, ids, table_q, table_s})) return fail(pc);
   v7g::launch_embedding_gather(out, ids, n_tokens, table_q, table_s, dim, vocab, stream());
   return check_launch();
 }
@@ -622,6 +692,10 @@ V7_ABI void v7s_embedding_row(float *out, int token, int dim, v7g_q8_tensor *q_d
   const float *s = q_desc->s + (base >> 6);
   if (!al16(out) || ((uintptr_t)q & 3u) || ((uintptr_t)s & 3u)) {
     fail(V7G_ERR_ALIGN);
+    return;
+  }
+  if (int pc = check_ptrs({out, q, s})) {
+    fail(pc);
     return;
   }
   v7g::launch_embedding_gather(out, nullptr, 1, q, s, dim, 1, stream());
