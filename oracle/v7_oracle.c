@@ -325,17 +325,44 @@ static float absf_bits(float v)
     return bits_to_float(u);
 }
 
+/* vmaxps / vmaxss dst, a, b: a > b ? a : b, so the second operand when either is NaN. */
+static float vmax(float a, float b)
+{
+    return (a > b) ? a : b;
+}
+
+/* Absmax of a full group, the vandps + vmaxps tree of quantize_kernel.inc:62-83 with its operand order,
+ * which decides where a NaN survives.  Eight-float vectors v_j = |x[8j .. 8j+7]|; for GS = 64:
+ * m = max(max(max(v0,v1), max(v2,v3)), max(max(v4,v5), max(v6,v7))) lane-wise, then lanes i and i+4
+ * (vextractf128), then 0,2 and 1,3 (vmovhlps), then 0 and 1 (vmovshdup).  GS = 32 takes the same shape over
+ * four vectors (the reference has no 32-element kernel); any other group size is scanned in order as the
+ * scalar tail scans (vmaxss |x|, wmax). */
+static float group_absmax(const float *x, int gs)
+{
+    if (gs == 64 || gs == 32) {
+        float m[8];
+        for (int i = 0; i < 8; ++i) {
+            float a[8];
+            for (int j = 0; j < gs / 8; ++j)
+                a[j] = absf_bits(x[8 * j + i]);
+            float lo = vmax(vmax(a[0], a[1]), vmax(a[2], a[3]));
+            m[i] = (gs == 64) ? vmax(lo, vmax(vmax(a[4], a[5]), vmax(a[6], a[7]))) : lo;
+        }
+        float p0 = vmax(m[0], m[4]), p1 = vmax(m[1], m[5]), p2 = vmax(m[2], m[6]), p3 = vmax(m[3], m[7]);
+        return vmax(vmax(p0, p2), vmax(p1, p3));
+    }
+    float w = 0.0f;
+    for (int i = 0; i < gs; ++i)
+        w = vmax(absf_bits(x[i]), w);
+    return w;
+}
+
 void orc_quantize(int8_t *out_q, const float *in_x, float *out_s, long long n, int gs)
 {
     long long full = n / gs;
     for (long long g = 0; g < full; ++g) {
         const float *x = in_x + g * gs;
-        /* absmax: vandps + vmaxps tree (:62-83); max is order-free on non-NaN input */
-        float wmax = absf_bits(x[0]);
-        for (int i = 1; i < gs; ++i) {
-            float a = absf_bits(x[i]);
-            wmax = (wmax > a) ? wmax : a;
-        }
+        float wmax = group_absmax(x, gs);
         wmax = (wmax > Q_FLOOR) ? wmax : Q_FLOOR; /* vmaxss wmax, eps (:84) */
         float scale = wmax / 127.0f;              /* vdivss (:86) */
         out_s[g] = scale;
@@ -348,10 +375,8 @@ void orc_quantize(int8_t *out_q, const float *in_x, float *out_s, long long n, i
         /* scalar tail, quantize_kernel.inc:119-152 */
         const float *x = in_x + full * gs;
         float wmax = 0.0f;
-        for (long long i = 0; i < rem; ++i) {
-            float a = absf_bits(x[i]);
-            wmax = (a > wmax) ? a : wmax; /* vmaxss xmm3, |x|, xmm3 */
-        }
+        for (long long i = 0; i < rem; ++i)
+            wmax = vmax(absf_bits(x[i]), wmax); /* vmaxss xmm3, |x|, xmm3 */
         wmax = (wmax > Q_FLOOR) ? wmax : Q_FLOOR;
         float scale = wmax / 127.0f;
         out_s[full] = scale;

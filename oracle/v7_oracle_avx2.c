@@ -200,9 +200,13 @@ AVX2 void orc_avx2_quantize(int8_t *out_q, const float *in_x, float *out_s, long
     long long full = n / gs;
     for (long long g = 0; g < full; ++g) {
         const float *x = in_x + g * gs;
-        __m256 m = _mm256_and_ps(absmask, _mm256_loadu_ps(x));
-        for (int i = 8; i < gs; i += 8)
-            m = _mm256_max_ps(m, _mm256_and_ps(absmask, _mm256_loadu_ps(x + i)));
+        __m256 v[8];
+        for (int j = 0; j < gs / 8; ++j)
+            v[j] = _mm256_and_ps(absmask, _mm256_loadu_ps(x + 8 * j));
+        /* the reference's pairing (quantize_kernel.inc:62-83), which fixes where a NaN survives */
+        __m256 m = _mm256_max_ps(_mm256_max_ps(v[0], v[1]), _mm256_max_ps(v[2], v[3]));
+        if (gs == 64)
+            m = _mm256_max_ps(m, _mm256_max_ps(_mm256_max_ps(v[4], v[5]), _mm256_max_ps(v[6], v[7])));
         __m128 l = _mm_max_ps(_mm256_castps256_ps128(m), _mm256_extractf128_ps(m, 1));
         l = _mm_max_ps(l, _mm_movehl_ps(l, l));
         l = _mm_max_ps(l, _mm_movehdup_ps(l));

@@ -291,9 +291,74 @@ def test_quantize_non_finite(ops, oracle):
     x[3, :] = 0.0
     wq, ws = oracle.quantize(x, 64)
     gq, gsc = ops.quantize_q8(dev(x), gs=64)
-    # rows without NaN: bit-exact (an Inf row gives scale Inf, codes 0 and -127 on both sides)
-    assert_bits(host(gq)[[0, 1, 3]], wq[[0, 1, 3]], "codes")
-    assert_bits(host(gsc)[[0, 1, 3]], ws[[0, 1, 3]], "scales")
+    # an Inf row gives scale Inf, codes 0 and -127; the NaN at element 63 reaches the group max through
+    # the reference's vmaxps tree, which the floor then replaces (scale 2^-126, every code -127)
+    assert_bits(host(gq), wq, "codes")
+    assert_bits(host(gsc), ws, "scales")
+    assert host(gsc)[2, 0] == np.float32(2.0 ** -126) and np.all(host(gq)[2] == -127)
+
+
+def nan_groups(seed, rows, row_len, gs):
+    """Rows of groups where a NaN sits at every position of the group in turn, beside a large value
+    (2^40, which a NaN can take out of the group max) and tiny ones (which the floor scale turns into
+    codes from 0 to -127 past 2^31); a third of the rows carry many NaN at random positions."""
+    x = C.normal(seed, (rows, row_len), 1.0)
+    rng = C.rng(seed + 1)
+    for r in range(rows):
+        for g0 in range(0, row_len - gs + 1, gs):
+            p = (r + g0 // gs) % gs
+            x[r, g0 + p] = np.nan
+            x[r, g0 + (p * 7 + 3 + r // gs) % gs] = np.float32(2.0 ** 40) * (1 - 2 * (r & 1))
+            x[r, g0 + (p + 1) % gs] = np.float32(3 * 2.0 ** -126)
+            x[r, g0 + (p + 2) % gs] = np.float32(2.0 ** -94)
+        if r % 3 == 2:
+            x[r, rng.integers(0, row_len, max(row_len // 8, 1))] = np.nan
+    return x
+
+
+@pytest.mark.parametrize("rows,row_len,gs", [(128, 128, 64), (64, 96, 32), (96, 1000, 64), (40, 1000, 32),
+                                             (16, 257, 16)])
+def test_quantize_nan_groups_follow_the_reference_tree(ops, oracle, rows, row_len, gs):
+    """A NaN in a group: the reference's vmaxps tree (src/asm/quantize_kernel.inc:62-84) lets it reach the
+    group max or drop out, with the values it was paired with, depending on its position.  Flat groups
+    (row_len a multiple of gs), groups of the general path (ragged rows) and their scalar tails, bit for bit."""
+    x = nan_groups(rows * row_len + gs, rows, row_len, gs)
+    wq, ws = oracle.quantize(x, gs)
+    gq, gsc = ops.quantize_q8(dev(x), gs=gs)
+    assert_bits(host(gq), wq, "codes")
+    assert_bits(host(gsc), ws, "scales")
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_swiglu_q8_nan_groups(ops, oracle, gs):
+    g = nan_groups(77 + gs, 64, 4096, gs)
+    u = C.normal(78 + gs, (64, 4096), 1.5)
+    u[5, 100:140] = np.nan
+    wq, ws = oracle.swiglu_q8(g, u, gs)
+    gq, gsc = ops.swiglu_q8(dev(g), dev(u), gs=gs)
+    assert_bits(host(gq), wq, "codes")
+    assert_bits(host(gsc), ws, "scales")
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_rmsnorm_quantize_nan_columns(ops, oracle, gs):
+    """NaN weights put a NaN at the same column of every row (the row's scale is unaffected), one NaN input
+    makes its whole row NaN: both follow the reference's tree (src/asm/rmsnorm_quantize_kernel.inc:158-187)."""
+    dim, rows = 2048, 2 * gs
+    x = C.normal(91, (rows, dim))
+    x[3, 17] = np.nan
+    w = C.norm_weight(92, dim)
+    w[np.arange(0, dim, dim // 32) + np.arange(32) % gs] = np.nan
+    wq, ws = oracle.rmsnorm_quantize(x, w, 1e-6, gs)
+    q, s = ops.rmsnorm_quantize(dev(x), dev(w), eps=1e-6, gs=gs)
+    assert_bits(host(q), wq, "codes")
+    assert_bits(host(s), ws, "scales")
+    r = C.normal(93, (rows, dim))
+    a = C.normal(94, (rows, dim))
+    wq, ws = oracle.rmsnorm_quantize(oracle.add_inplace(r, a), w, 1e-6, gs)
+    q, s = ops.add_rmsnorm_quantize(dev(r), dev(a), dev(w), eps=1e-6, gs=gs)
+    assert_bits(host(q), wq, "codes")
+    assert_bits(host(s), ws, "scales")
 
 
 @pytest.mark.parametrize("gs", [32, 64])

@@ -488,6 +488,58 @@ def test_quantize_ties_to_even_and_nan_codes(oracle):
     assert q[0, 0] == -127 and q[0, 64 + 5] == -127
 
 
+def test_quantize_nan_position_in_the_max_tree(oracle):
+    """vmaxps returns its second operand when either is NaN, so the group max of the vector path depends
+    on where a NaN sits (src/asm/quantize_kernel.inc:62-84 and the note at :128).  Hand-traced cases:
+    - NaN at element 63 (vector 7, lane 7) is the second operand at every level of the tree: wmax is NaN,
+      vmaxss wmax, eps gives the floor 127*2^-126, scale 2^-126, reciprocal 2^126.  Codes are then
+      rne(x * 2^126) saturated: 3*2^-126 -> 3, 2^-120 -> 64, 2^-100 -> 127, -2^-100 -> -127, and
+      2^-94 or 1.0 -> -127 (beyond 2^31 vcvtps2dq gives 0x80000000, whatever the sign);
+    - the same for element 31 of a 32-element group (vector 3, lane 7);
+    - NaN at element 62 (lane 6) reaches vmaxps(p0, p2) as p2 and then is the first operand of the last
+      vmaxps: it drops out, wmax = 1;
+    - NaN at element 8 (vector 1, lane 0) survives vmaxps(v0, v1) and drops out at the next level, taking
+      element 0 with it: wmax = 1 although x[0] = 2^40, whose code is then -127;
+    - NaN at element 16 (vector 2) is the first operand of vmaxps(v2, v3) and drops out alone: wmax is
+      x[0] = 2^40 (an in-order scan of the vectors would have lost it);
+    - the scalar tail (vmaxss |x|, wmax) and the in-order scan of other group sizes always drop a NaN."""
+    tiny = np.array([3 * 2.0 ** -126, 2.0 ** -120, 2.0 ** -100, -2.0 ** -100, 2.0 ** -94, 0.0, 1.0], F)
+    tiny_codes = np.array([3, 64, 127, -127, -127, 0, -127], np.int8)
+    for gs, at in ((64, 63), (32, 31)):
+        x = np.ones(gs, F)
+        x[:7] = tiny
+        x[at] = np.nan
+        q, s = oracle.quantize(x[None], gs)
+        assert s[0, 0] == np.float32(2.0 ** -126)
+        assert bits_equal(q[0, :7], tiny_codes) and np.all(q[0, 7:] == -127)
+    one_127 = np.float32(1.0) / np.float32(127.0)
+    x = np.ones(64, F)
+    x[62] = np.nan
+    q, s = oracle.quantize(x[None], 64)
+    assert s[0, 0] == one_127 and q[0, 62] == -127 and np.all(np.delete(q[0], 62) == 127)
+    for gs in (64, 32):
+        x = np.ones(gs, F)
+        x[0] = 2.0 ** 40
+        x[8] = np.nan
+        q, s = oracle.quantize(x[None], gs)
+        assert s[0, 0] == one_127 and q[0, 0] == -127 and q[0, 8] == -127
+        assert np.all(np.delete(q[0], [0, 8]) == 127)
+        x[8] = 1.0
+        x[16] = np.nan
+        q, s = oracle.quantize(x[None], gs)
+        assert s[0, 0] == np.float32(2.0 ** 40) / np.float32(127.0) and q[0, 0] == 127 and q[0, 16] == -127
+        assert np.all(np.delete(q[0], [0, 16]) == 0)
+    x = np.ones(16, F)
+    x[15] = np.nan
+    x[3] = 2.0
+    q, s = oracle.quantize(x[None], 16)
+    assert s[0, 0] == np.float32(2.0) / np.float32(127.0) and q[0, 3] == 127 and q[0, 15] == -127
+    x = np.ones(64 + 10, F)
+    x[-1] = np.nan
+    q, s = oracle.quantize(x[None], 64)
+    assert s[0, 1] == one_127 and q[0, -1] == -127 and np.all(q[0, 64:-1] == 127)
+
+
 def test_swiglu_q8_is_quantize_of_swiglu_and_near_double(oracle):
     g = C.normal(401, (16, 8192), 1.5)
     u = C.normal(402, (16, 8192), 1.5)
@@ -541,6 +593,13 @@ def test_avx2_matches_scalar_oracle(oracle):
     xq = C.normal(8, (5, 8192 + 40), 2.0)
     for gs in (32, 64):
         assert all(bits_equal(p, q) for p, q in zip(oracle.avx2_quantize(xq, gs), oracle.quantize(xq, gs)))
+    # NaN sprinkled over the groups: the hardware vmaxps of the AVX2 form against the scalar tree
+    xn = xq.copy()
+    pick = C.rng(11).integers(0, xn.size, 600)
+    xn.reshape(-1)[pick] = np.nan
+    xn.reshape(-1)[pick[:200] + 1] = C.rng(12).uniform(1e3, 1e12, 200).astype(F)
+    for gs in (32, 64):
+        assert all(bits_equal(p, q) for p, q in zip(oracle.avx2_quantize(xn, gs), oracle.quantize(xn, gs)))
     tq, ts = C.q8_table(9, 100, 512)
     ids = C.rng(10).integers(0, 100, 20).astype(np.int32)
     assert bits_equal(oracle.avx2_embedding_gather(ids, tq, ts, 512), oracle.embedding_gather(ids, tq, ts, 512))

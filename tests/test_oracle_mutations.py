@@ -108,6 +108,15 @@ MUTANTS = [
     ("quant: no floor",
      "        wmax = (wmax > Q_FLOOR) ? wmax : Q_FLOOR; /* vmaxss wmax, eps (:84) */",
      "        wmax = (wmax > 0.0f) ? wmax : 1e-30f;"),
+    ("quant: NaN-free max",
+     "    return (a > b) ? a : b;",
+     "    return fmaxf(a, b);"),
+    ("quant: vectors scanned in order",
+     "            float lo = vmax(vmax(a[0], a[1]), vmax(a[2], a[3]));",
+     "            float lo = vmax(vmax(vmax(a[0], a[1]), a[2]), a[3]);"),
+    ("quant: lanes i+4 first",
+     "        float p0 = vmax(m[0], m[4]), p1 = vmax(m[1], m[5]), p2 = vmax(m[2], m[6]), p3 = vmax(m[3], m[7]);",
+     "        float p0 = vmax(m[4], m[0]), p1 = vmax(m[5], m[1]), p2 = vmax(m[6], m[2]), p3 = vmax(m[7], m[3]);"),
     ("quant: recip from wmax",
      "        float recip = 1.0f / scale;               /* vdivss (:88) */",
      "        float recip = 127.0f / wmax;"),

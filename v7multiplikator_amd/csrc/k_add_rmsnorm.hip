@@ -110,16 +110,23 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
     } else {
       // QGS/4 consecutive lanes hold one group (dim % QGS == 0 and TPR % 16 == 0:
       // a group is entirely live or entirely past the row); every lane takes
-      // part in the DPP butterfly.
+      // part in the DPP butterfly, or, in a wave holding a NaN, in the
+      // reference's ordered vmaxps tree (rmsnorm_quantize_kernel.inc:158-186).
       constexpr int LPG = QGS / 4;
-      float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(n.x), __builtin_fabsf(n.y)),
-                                __builtin_fmaxf(__builtin_fabsf(n.z), __builtin_fabsf(n.w)));
-      m = (LPG == 8) ? group8_max(m) : group16_max(m);
+      float m = lane_absmax4(n);
       float scale, recip;
-      q8_scale(m, scale, recip);
+      uint32_t codes;
+      if (!wave_any_nan(m)) {
+        m = (LPG == 8) ? group8_max(m) : group16_max(m);
+        q8_scale(m, scale, recip);
+        codes = pack4_codes(n, recip);
+      } else {
+        q8_scale(q8_floor(group_absmax_tree<QGS>(n)), scale, recip);
+        codes = pack4_codes_full(n, recip);
+      }
       if (live) {
         const size_t c = (r * (size_t)dim + i) >> 2;  // dword of 4 codes
-        st_stream_u32(reinterpret_cast<uint32_t *>(q) + c, pack4_codes(n, recip));
+        st_stream_u32(reinterpret_cast<uint32_t *>(q) + c, codes);
         if ((tid & (LPG - 1)) == 0) st_stream_f32(q_s + r * (size_t)(dim / QGS) + (i / QGS), scale);
       }
     }

@@ -15,8 +15,9 @@
 //
 // Vector layout: lane owns 4 consecutive floats (streaming dwordx4 loads of
 // gate and up, or x), GS/4 consecutive lanes form one group, the group max is
-// a DPP butterfly inside 8 or 16 lanes, each lane stores its 4 codes as one
-// dword, and the first lane of the group stores the scale.  The divisions of
+// a DPP butterfly inside 8 or 16 lanes (the reference's ordered vmaxps tree in
+// a wave that holds a NaN), each lane stores its 4 codes as one dword, and the
+// first lane of the group stores the scale.  The divisions of
 // the reference (sigmoid's 1/(1+e), wmax/127, 1/scale) are the shorter
 // sequences of v7g_device.h that give the same bits for every reachable input.
 #include "v7g_device.h"
@@ -104,21 +105,32 @@ __global__ __launch_bounds__(kStreamBlock) void quantize_q8_flat_kernel(int8_t *
     } else {
       v = ld_stream4(x + 4 * c);
     }
-    // absmax (vandps + vmaxps tree, order-free for non-NaN input)
-    float m = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
-                              __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
-    m = (LPG == 8) ? group8_max(m) : group16_max(m);
+    // absmax: without NaN the vmaxps tree is a plain maximum, a DPP butterfly
+    // here; a wave holding a NaN takes the reference's ordered tree instead.
+    float m = lane_absmax4(v);
     float scale, recip;
-    q8_scale(m, scale, recip);
-    st_stream_u32(reinterpret_cast<uint32_t *>(out_q) + c, pack4_codes(v, recip));
+    uint32_t codes;
+    if (!wave_any_nan(m)) {
+      m = (LPG == 8) ? group8_max(m) : group16_max(m);
+      q8_scale(m, scale, recip);
+      codes = pack4_codes(v, recip);
+    } else {
+      q8_scale(q8_floor(group_absmax_tree<GS>(v)), scale, recip);
+      codes = pack4_codes_full(v, recip);
+    }
+    st_stream_u32(reinterpret_cast<uint32_t *>(out_q) + c, codes);
     if ((threadIdx.x & (LPG - 1)) == 0) st_stream_f32(out_s + c / LPG, scale);
   }
 }
 
 // General path: any row length, any GS in [1, 4096]; one thread per group,
-// scalar loads.  A partial last group of a row takes the reference's scalar
-// tail arithmetic (quantize_kernel.inc:119-152), value-identical to the
-// vector path for every non-NaN input.
+// scalar loads.  A full group of 32 or 64 takes the reference's ordered vmaxps
+// tree; any other group, and a partial last group of a row, scans in order as
+// the reference's scalar tail does (quantize_kernel.inc:119-152: vmaxss |x|,
+// wmax drops a NaN element), which for non-NaN input is the same maximum.
+// The codes of a tail group cannot leave [-127.00002, 127.00002] except as
+// NaN, where the tail's vmaxss/vminss/vcvtss2si and the vector conversion both
+// give -127, so one conversion serves both.
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void quantize_q8_generic_kernel(int8_t *out_q, float *out_s, const float *x,
                                                                   const float *gate, const float *up, int rows,
@@ -130,18 +142,26 @@ __global__ __launch_bounds__(256) void quantize_q8_generic_kernel(int8_t *out_q,
   const int g = (int)(gid - r * spr);
   const long long start = r * row_len + (long long)g * gs;
   const int len = min(gs, row_len - g * gs);
+  auto value = [&](int i) { return SWIGLU ? swiglu_v7(gate[start + i], up[start + i]) : x[start + i]; };
   float wmax = 0.0f;
-  for (int i = 0; i < len; ++i) {
-    float v = SWIGLU ? swiglu_v7(gate[start + i], up[start + i]) : x[start + i];
-    wmax = __builtin_fmaxf(wmax, __builtin_fabsf(v));
+  if (len == gs && (gs == 32 || gs == 64)) {
+    // class maxima over vectors j = 0 .. gs/8-1, paired (0,1), (2,3), then
+    // (01, 23), and (0123, 4567); then lanes i with i+4, 0 with 2 and 1 with 3, 0 with 1
+    float m[8];
+    for (int i = 0; i < 8; ++i) {
+      auto a = [&](int j) { return __builtin_fabsf(value(8 * j + i)); };
+      const float lo = vmax_x86(vmax_x86(a(0), a(1)), vmax_x86(a(2), a(3)));
+      m[i] = gs == 64 ? vmax_x86(lo, vmax_x86(vmax_x86(a(4), a(5)), vmax_x86(a(6), a(7)))) : lo;
+    }
+    wmax = vmax_x86(vmax_x86(vmax_x86(m[0], m[4]), vmax_x86(m[2], m[6])),
+                    vmax_x86(vmax_x86(m[1], m[5]), vmax_x86(m[3], m[7])));
+  } else {
+    for (int i = 0; i < len; ++i) wmax = vmax_x86(__builtin_fabsf(value(i)), wmax);
   }
   float scale, recip;
-  q8_scale(wmax, scale, recip);
+  q8_scale(q8_floor(wmax), scale, recip);
   out_s[r * spr + g] = scale;
-  for (int i = 0; i < len; ++i) {
-    float v = SWIGLU ? swiglu_v7(gate[start + i], up[start + i]) : x[start + i];
-    out_q[start + i] = (int8_t)q8_code(v * recip);
-  }
+  for (int i = 0; i < len; ++i) out_q[start + i] = (int8_t)q8_code_byte_full(value(i) * recip);
 }
 
 template <int GS>

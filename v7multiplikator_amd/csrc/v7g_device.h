@@ -80,8 +80,12 @@ __device__ __forceinline__ float swiglu_v7(float g, float u) {
 // Per-group scale and reciprocal, src/asm/quantize_kernel.inc:84-89:
 // wmax = max(wmax, floor); scale = wmax / 127; recip = 1 / scale.  An Inf
 // group max (an Inf input) gives scale Inf and recip 0, as IEEE division does.
+// wmax is a maximum of magnitudes and not NaN (a NaN group max first goes
+// through vmaxss wmax, floor, which gives the floor: q8_floor below), so the
+// max with the floor compares the bit patterns as unsigned integers.
 __device__ __forceinline__ void q8_scale(float wmax, float &scale, float &recip) {
-  wmax = __builtin_fmaxf(wmax, V7G_Q_FLOOR);
+  const uint32_t wb = __builtin_bit_cast(uint32_t, wmax), fb = __builtin_bit_cast(uint32_t, V7G_Q_FLOOR);
+  wmax = __builtin_bit_cast(float, __builtin_elementwise_max(wb, fb));
   const bool inf = wmax == __builtin_inff();
   scale = inf ? wmax : div127_rn(wmax);
   recip = inf ? 0.0f : rcp_rn(scale);
@@ -104,6 +108,25 @@ __device__ __forceinline__ uint32_t pack4_codes(float4 v, float recip) {
   return q8_code_byte(v.x * recip) | (q8_code_byte(v.y * recip) << 8) | (q8_code_byte(v.z * recip) << 16) |
          (q8_code_byte(v.w * recip) << 24);
 }
+
+// The same code for any v, also beyond +-127.00002 (a group whose max lost
+// elements to a NaN, below): vcvtps2dq gives 0x80000000 for NaN and for
+// |v| >= 2^31, which the packs and vpmaxsb turn into -127; in range,
+// rne(v) saturates to [-127, 127], and clamping before rounding gives the same.
+__device__ __forceinline__ uint32_t q8_code_byte_full(float v) {
+  const bool in_range = v >= -2147483648.0f && v < 2147483648.0f;
+  return in_range ? q8_code_byte(__builtin_amdgcn_fmed3f(v, -127.0f, 127.0f)) : 0x81u;
+}
+__device__ __forceinline__ uint32_t pack4_codes_full(float4 v, float recip) {
+  return q8_code_byte_full(v.x * recip) | (q8_code_byte_full(v.y * recip) << 8) |
+         (q8_code_byte_full(v.z * recip) << 16) | (q8_code_byte_full(v.w * recip) << 24);
+}
+
+// vmaxps / vmaxss a, b: a > b ? a : b, the second operand when either is NaN.
+__device__ __forceinline__ float vmax_x86(float a, float b) { return (a > b) ? a : b; }
+
+// vmaxss wmax, floor (quantize_kernel.inc:84) for a group max that may be NaN.
+__device__ __forceinline__ float q8_floor(float wmax) { return vmax_x86(wmax, V7G_Q_FLOOR); }
 
 // binary32 -> binary16 with round to nearest even (v_cvt_f16_f32 in the
 // default rounding mode, binary16 subnormals kept), the conversion of the
@@ -153,24 +176,27 @@ enum : int {
 };
 
 template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return __builtin_elementwise_max(a, b); }
+
+// Max over aligned groups of 8 lanes of non-negative, non-NaN floats: their
+// bit patterns order as unsigned integers do, so each step is one
+// v_max_u32 with a DPP operand (order-free, and no NaN quieting).
+__device__ __forceinline__ float group8_max(float f) {
+  uint32_t v = __builtin_bit_cast(uint32_t, f);
+  v = umax(v, dpp_u<DPP_QUAD_XOR1>(v));
+  v = umax(v, dpp_u<DPP_QUAD_XOR2>(v));
+  v = umax(v, dpp_u<DPP_ROW_HALF_MIRROR>(v));
+  return __builtin_bit_cast(float, v);
 }
 
-// max over aligned groups of 8 lanes (order-free for non-NaN input).
-__device__ __forceinline__ float group8_max(float v) {
-  v = __builtin_fmaxf(v, dpp_f<DPP_QUAD_XOR1>(v));
-  v = __builtin_fmaxf(v, dpp_f<DPP_QUAD_XOR2>(v));
-  v = __builtin_fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
-  return v;
-}
-
-// max over aligned groups of 16 lanes.
-__device__ __forceinline__ float group16_max(float v) {
-  v = group8_max(v);
-  v = __builtin_fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
-  return v;
+// The same over aligned groups of 16 lanes.
+__device__ __forceinline__ float group16_max(float f) {
+  uint32_t v = __builtin_bit_cast(uint32_t, group8_max(f));
+  v = umax(v, dpp_u<DPP_ROW_MIRROR>(v));
+  return __builtin_bit_cast(float, v);
 }
 
 // Lane exchange by xor inside the wave (ds_bpermute); exact pairing for the
@@ -178,6 +204,48 @@ __device__ __forceinline__ float group16_max(float v) {
 __device__ __forceinline__ float xor_f(float v, int mask) {
   int lane = __lane_id();
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, v)));
+}
+
+// |x|, |y|, |z|, |w| reduced with v_maximum3_f32, which propagates NaN: the
+// lane's share of a group max, NaN exactly when one of its elements is NaN.
+__device__ __forceinline__ float lane_absmax4(float4 v) {
+  return __builtin_elementwise_maximum(
+      __builtin_elementwise_maximum(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+      __builtin_elementwise_maximum(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+}
+
+// True for every lane of the wave when some lane's value is NaN.
+__device__ __forceinline__ bool wave_any_nan(float m) { return __builtin_amdgcn_ballot_w64(m != m) != 0; }
+
+// One level of an ordered max tree across lanes l and l ^ MASK: the lane with
+// the bit clear supplies the first operand, so both lanes get the same value.
+template <int MASK>
+__device__ __forceinline__ float tree_max_step(float a) {
+  const float o = xor_f(a, MASK);
+  return (__lane_id() & MASK) ? vmax_x86(o, a) : vmax_x86(a, o);
+}
+
+// Group absmax with the reference's vmaxps tree and operand order
+// (src/asm/quantize_kernel.inc:62-83, src/asm/rmsnorm_quantize_kernel.inc:158-186).
+// Without NaN it is the plain maximum; with NaN, the operand order decides
+// whether the NaN reaches wmax (which the floor then replaces) or drops out
+// together with the values it was paired with.  The group's GS/4 lanes hold 4
+// consecutive elements each: element e = 4l + k is lane i = e % 8 = 4(l&1) + k
+// of YMM vector j = e / 8 = l/2.  The per-lane levels pair vectors j^1, j^2,
+// j^4 (lanes l^2, l^4, l^8; GS = 32 stops after j^2), vextractf128 pairs lane
+// i with i+4 (lanes l^1), and vmovhlps / vmovshdup pair components k with k+2,
+// then 0 with 1, inside the lane.  Every lane of the group returns the value.
+template <int GS>
+__device__ __forceinline__ float group_absmax_tree(float4 v) {
+  float a[4] = {__builtin_fabsf(v.x), __builtin_fabsf(v.y), __builtin_fabsf(v.z), __builtin_fabsf(v.w)};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    a[k] = tree_max_step<2>(a[k]);
+    a[k] = tree_max_step<4>(a[k]);
+    if constexpr (GS == 64) a[k] = tree_max_step<8>(a[k]);
+    a[k] = tree_max_step<1>(a[k]);
+  }
+  return vmax_x86(vmax_x86(a[0], a[2]), vmax_x86(a[1], a[3]));
 }
 
 // COMPUTE_RMS_SCALE, src/asm/v7_macros.inc:348-354: 1 / sqrt(sumsq/n + eps),
