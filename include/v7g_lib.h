@@ -257,7 +257,8 @@ int v7g_add_inplace(float *x, const float *y, long long n);
  * start at buf + t*token_stride (floats) and are contiguous.  Position of token
  * t: positions[t] (device int32 array) or, if positions is NULL, pos0 + t.
  * Tables: table_rows rows of rope_max_dim floats (a position outside the tables
- * yields NaN heads). */
+ * yields NaN heads).  head_dim % 32 == 0 in [64, 512]; n_tokens times the
+ * heads per token (of every side, for the Q/K and Q/K/V forms) < 2^28. */
 int v7g_rmsnorm_rope_heads(float *buf, int n_tokens, long long token_stride, int n_heads, int head_dim,
                            const float *norm_weight, const float *cos_table, const float *sin_table,
                            const int32_t *positions, int pos0, int rope_max_dim, int table_rows, float eps);

@@ -129,6 +129,14 @@ def test_rope_rejects_short_table_rows_and_stride(L):
                    0, 64, 16, 1e-6)[0] == 1
 
 
+@pytest.mark.skipif("__import__('torch').cuda.is_available()",
+                    reason="a missed check would launch on the fake pointers; run where no GPU is present")
+def test_rope_head_count_sums_cannot_overflow(L):
+    """Q + K (+ V) head counts add in 64 bits: 2^30 + 2^30 heads per token is rejected, not wrapped negative."""
+    assert _sticky(L, L.v7g_qk_rmsnorm_rope, FAKE, 4096, 1 << 30, FAKE, FAKE, 1024, 1 << 30, FAKE, 1, 128, FAKE,
+                   FAKE, None, 0, 64, 16, 1e-6) == (2, 2)
+
+
 def test_quantize_and_swiglu_reject(L):
     assert _sticky(L, L.v7g_quantize_q8, FAKE, FAKE, FAKE, 1, 64, 0)[0] == 2
     assert _sticky(L, L.v7g_quantize_q8, FAKE, FAKE, FAKE, 1, 64, 8192)[0] == 2

@@ -117,8 +117,10 @@ int check_rope_common(int n_tokens, int head_dim, const float *cos_table, const 
 }
 
 // 8 lanes per head: the grid of n_tokens * heads_per_token heads must stay below 2^32 threads.
-int check_rope_heads(int n_tokens, int heads_per_token) {
-  return (long long)n_tokens * heads_per_token >= (1LL << 28) ? V7G_ERR_SHAPE : V7G_OK;
+// heads_per_token is the sum of the sides' head counts, taken in 64 bits by the callers.
+int check_rope_heads(int n_tokens, long long heads_per_token) {
+  return (heads_per_token >= (1LL << 28) || (long long)n_tokens * heads_per_token >= (1LL << 28)) ? V7G_ERR_SHAPE
+                                                                                                  : V7G_OK;
 }
 
 int check_rope_side(const float *buf, long long token_stride, int n_heads, int head_dim, const float *w,
@@ -245,6 +247,9 @@ int own_tables(int n_pos, const std::vector<double> &freq) {
 }
 
 hipStream_t stream() { return g_stream; }
+
+// Table rows 0..pos for the one-token drop-in entries, without overflowing at INT_MAX.
+int rows_through(int pos) { return pos < 2147483647 ? pos + 1 : pos; }
 
 }  // namespace
 
@@ -439,7 +444,7 @@ int v7g_qk_rmsnorm_rope(float *q, long long q_token_stride, int n_q_heads, const
   int rc = check_rope_common(n_tokens, head_dim, cos_table, sin_table, rope_max_dim, table_rows);
   if (!rc) rc = check_rope_side(q, q_token_stride, n_q_heads, head_dim, q_norm_weight, n_tokens);
   if (!rc) rc = check_rope_side(k, k_token_stride, n_kv_heads, head_dim, k_norm_weight, n_tokens);
-  if (!rc) rc = check_rope_heads(n_tokens, n_q_heads + n_kv_heads);
+  if (!rc) rc = check_rope_heads(n_tokens, (long long)n_q_heads + n_kv_heads);
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
@@ -496,7 +501,8 @@ int v7g_qkv_rope_stage(const v7g_qkv_stage *st) {
   if (!rc) rc = check_stage_side(st->q, st->n_tokens, st->head_dim, true, false);
   if (!rc) rc = check_stage_side(st->k, st->n_tokens, st->head_dim, true, true);
   if (!rc && has_v) rc = check_stage_side(st->v, st->n_tokens, st->head_dim, false, true);
-  if (!rc) rc = check_rope_heads(st->n_tokens, st->q.n_heads + st->k.n_heads + (has_v ? st->v.n_heads : 0));
+  if (!rc)
+    rc = check_rope_heads(st->n_tokens, (long long)st->q.n_heads + st->k.n_heads + (has_v ? st->v.n_heads : 0));
   if (!rc && st->positions && ((uintptr_t)st->positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (st->n_tokens == 0) return V7G_OK;
@@ -628,7 +634,7 @@ V7_ABI void v7s_rope_only_heads(float *buf, int n_heads, int head_dim, float *co
     return;
   }
   v7g_rope_only_heads(buf, 1, (long long)n_heads * head_dim, n_heads, head_dim, cos_table, sin_table, nullptr, pos,
-                      rope_max_dim, pos + 1);
+                      rope_max_dim, rows_through(pos));
 }
 
 V7_ABI void v7s_kv_pack_f16(uint16_t *dest, float *src, int count) {
@@ -665,7 +671,7 @@ V7_ABI void v7s_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, float 
   // The caller's tables hold at least pos+1 rows (the reference offsets them by
   // pos*rope_max_dim without a bound).
   v7g_rmsnorm_rope_heads(buf, 1, (long long)n_heads * head_dim, n_heads, head_dim, norm_weight, cos_table, sin_table,
-                         nullptr, pos, rope_max_dim, pos + 1, g_eps.load());
+                         nullptr, pos, rope_max_dim, rows_through(pos), g_eps.load());
 }
 
 V7_ABI void v7d_quantize(char *out_q, float *in_x, float *out_s, int n) {
