@@ -777,3 +777,39 @@ def test_pointer_checks_reject_host_memory(ops):
     finally:
         L.v7g_set_pointer_checks(0)
         L.v7g_clear_last_error()
+
+
+def test_torch_ops_reject_undersized_outputs_and_mismatched_tables(ops):
+    """The torch-facing functions refuse, before any launch, buffers the kernels would overrun: outputs of
+    another shape, norm weights that are not [head_dim], cos/sin tables of different shapes."""
+    r = torch.zeros((4, 256), device="cuda")
+    a = torch.zeros((4, 256), device="cuda")
+    w = torch.ones(256, device="cuda")
+    with pytest.raises(ValueError):
+        ops.fused_add_rmsnorm(r, a, w, out=torch.empty((2, 256), device="cuda"))
+    with pytest.raises(ValueError):
+        ops.swiglu(r, a, out=torch.empty(100, device="cuda"))
+    ids = torch.zeros(3, dtype=torch.int32, device="cuda")
+    tq = torch.zeros((10, 128), dtype=torch.int8, device="cuda")
+    ts = torch.ones(10 * 2, device="cuda")
+    with pytest.raises(ValueError):
+        ops.embedding_gather_q8(ids, tq, ts, out=torch.empty((2, 128), device="cuda"))
+    q = torch.zeros((2, 4, 128), device="cuda")
+    k = torch.zeros((2, 2, 128), device="cuda")
+    qw = torch.ones(128, device="cuda")
+    c = torch.ones((4, 64), device="cuda")
+    with pytest.raises(ValueError):
+        ops.rmsnorm_rope_heads(q, torch.ones(64, device="cuda"), c, c)
+    with pytest.raises(ValueError):
+        ops.rmsnorm_rope_heads(q, qw, c, torch.ones((2, 64), device="cuda"))
+    with pytest.raises(ValueError):
+        ops.qk_rmsnorm_rope(q, k, qw, torch.ones(96, device="cuda"), c, c)
+    with pytest.raises(ValueError):
+        ops.rope_only_heads(q, c, torch.ones((4, 32), device="cuda"))
+    with pytest.raises(ValueError):
+        ops.qkv_rope_stage(q, k, None, c, c, q_norm_weight=torch.ones(64, device="cuda"))
+    torch.cuda.synchronize()
+    # the valid calls still run
+    ops.rmsnorm_rope_heads(q, qw, c, c)
+    ops.fused_add_rmsnorm(r, a, w)
+    torch.cuda.synchronize()

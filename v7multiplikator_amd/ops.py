@@ -69,6 +69,8 @@ def fused_add_rmsnorm(residual: torch.Tensor, add: torch.Tensor, weight: torch.T
     if out is None:
         out = torch.empty_like(residual)
     _need(out, torch.float32, "out")
+    if out.shape != residual.shape:
+        raise ValueError("out must match residual")
     _bind(residual)
     rc = _lib.load().v7g_fused_add_rmsnorm(out.data_ptr(), residual.data_ptr(), add.data_ptr(), weight.data_ptr(),
                                            rows, dim, float(eps))
@@ -148,6 +150,19 @@ def _heads_view(buf: torch.Tensor, name: str):
     return T, H, D, buf.stride(0)
 
 
+def _tables(cos_table: torch.Tensor, sin_table: torch.Tensor) -> None:
+    for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
+        _need(t, torch.float32, n)
+    if cos_table.dim() != 2 or sin_table.shape != cos_table.shape:
+        raise ValueError("cos_table and sin_table must both be [positions, rope_max_dim]")
+
+
+def _head_weight(w: torch.Tensor, D: int, name: str) -> None:
+    _need(w, torch.float32, name)
+    if w.numel() != D:
+        raise ValueError(f"{name} must hold head_dim = {D} floats")
+
+
 def _positions(positions, T, device):
     if positions is None:
         return 0
@@ -162,9 +177,9 @@ def rmsnorm_rope_heads(buf: torch.Tensor, norm_weight: torch.Tensor, cos_table: 
                        eps: float = 1e-6) -> torch.Tensor:
     """In-place per-head RMSNorm + RoPE of buf [T, H, D] (token stride free); tables [P, rope_max_dim]."""
     _need(buf, torch.float32, "buf", contiguous=False)
-    for t, n in ((norm_weight, "norm_weight"), (cos_table, "cos_table"), (sin_table, "sin_table")):
-        _need(t, torch.float32, n)
+    _tables(cos_table, sin_table)
     T, H, D, ts = _heads_view(buf, "buf")
+    _head_weight(norm_weight, D, "norm_weight")
     _bind(buf)
     rc = _lib.load().v7g_rmsnorm_rope_heads(buf.data_ptr(), T, ts, H, D, norm_weight.data_ptr(),
                                             cos_table.data_ptr(), sin_table.data_ptr(),
@@ -185,13 +200,13 @@ def qk_rmsnorm_rope(q: torch.Tensor, k: torch.Tensor, q_norm_weight: torch.Tenso
     untouched."""
     for t, n in ((q, "q"), (k, "k")):
         _need(t, torch.float32, n, contiguous=False)
-    for t, n in ((q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight"), (cos_table, "cos_table"),
-                 (sin_table, "sin_table")):
-        _need(t, torch.float32, n)
+    _tables(cos_table, sin_table)
     T, Hq, D, qs = _heads_view(q, "q")
     Tk, Hk, Dk, ks = _heads_view(k, "k")
     if Tk != T or Dk != D:
         raise ValueError("q and k must have the same tokens and head_dim")
+    _head_weight(q_norm_weight, D, "q_norm_weight")
+    _head_weight(k_norm_weight, D, "k_norm_weight")
     _bind(q)
     if k_cache is None:
         rc = _lib.load().v7g_qk_rmsnorm_rope(q.data_ptr(), qs, Hq, q_norm_weight.data_ptr(), k.data_ptr(), ks, Hk,
@@ -221,6 +236,8 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None
     if out is None:
         out = torch.empty_like(gate)
     _need(out, torch.float32, "out")
+    if out.shape != gate.shape:
+        raise ValueError("out must match gate")
     _bind(gate)
     rc = _lib.load().v7g_swiglu_f32(out.data_ptr(), gate.data_ptr(), up.data_ptr(), gate.numel())
     _lib.check(rc, "swiglu")
@@ -286,6 +303,8 @@ def embedding_gather_q8(ids: torch.Tensor, table_q: torch.Tensor, table_s: torch
     if out is None:
         out = torch.empty((n, dim), dtype=torch.float32, device=ids.device)
     _need(out, torch.float32, "out")
+    if out.numel() != n * dim:
+        raise ValueError("out must hold [ids, dim] floats")
     _bind(ids)
     rc = _lib.load().v7g_embedding_gather_q8(out.data_ptr(), ids.data_ptr(), n, table_q.data_ptr(),
                                              table_s.data_ptr(), dim, vocab)
@@ -297,8 +316,7 @@ def rope_only_heads(buf: torch.Tensor, cos_table: torch.Tensor, sin_table: torch
                     positions: torch.Tensor | None = None, pos0: int = 0) -> torch.Tensor:
     """In-place RoPE (no per-head norm) of buf [T, H, D]; tables [P, rope_max_dim]."""
     _need(buf, torch.float32, "buf", contiguous=False)
-    for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
-        _need(t, torch.float32, n)
+    _tables(cos_table, sin_table)
     T, H, D, ts = _heads_view(buf, "buf")
     _bind(buf)
     rc = _lib.load().v7g_rope_only_heads(buf.data_ptr(), T, ts, H, D, cos_table.data_ptr(), sin_table.data_ptr(),
@@ -316,7 +334,7 @@ def _side(buf, norm_weight, bias, cache, keep, name):
     T, H, D, ts = _heads_view(buf, name)
     side.buf, side.token_stride, side.n_heads, side.keep_f32 = buf.data_ptr(), ts, H, int(bool(keep))
     if norm_weight is not None:
-        _need(norm_weight, torch.float32, f"{name} norm_weight")
+        _head_weight(norm_weight, D, f"{name} norm_weight")
         side.norm_weight = norm_weight.data_ptr()
     if bias is not None:
         _need(bias, torch.float32, f"{name} bias")
@@ -338,8 +356,7 @@ def qkv_rope_stage(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, cos
                    v_cache=None, keep_k_f32: bool = True, keep_v_f32: bool = True) -> None:
     """The Q/K/V stage of a prefill over T tokens in one launch: bias add (optional, per side), Q and K
     RMSNorm+RoPE (norm weight given) or RoPE only, binary16 K/V cache rows (optional); all in place."""
-    for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
-        _need(t, torch.float32, n)
+    _tables(cos_table, sin_table)
     st = _lib.QkvStage()
     st.q, shq = _side(q, q_norm_weight, q_bias, None, True, "q")
     st.k, shk = _side(k, k_norm_weight, k_bias, k_cache, keep_k_f32, "k")
