@@ -70,6 +70,8 @@ def lib():
             "orc_avx2_swiglu": (None, [_f32p, _f32p, _f32p, c_ll]),
             "orc_avx2_quantize": (None, [_i8p, _f32p, _f32p, c_ll, c_int]),
             "orc_avx2_embedding_row": (None, [_f32p, c_int, c_int, _i8p, _f32p]),
+            "orc_set_reference_fp_env": (None, [c_int]),
+            "orc_get_reference_fp_env": (c_int, []),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -77,6 +79,20 @@ def lib():
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+class gradual_underflow:
+    """Context manager: the oracle's path functions run with IEEE gradual underflow instead of the
+    reference's MXCSR FTZ+DAZ (v7_oracle.h), to show what that mode changes."""
+
+    def __enter__(self):
+        self._old = lib().orc_get_reference_fp_env()
+        lib().orc_set_reference_fp_env(0)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_reference_fp_env(self._old)
+        return False
 
 
 def _c(a, dt):

@@ -9,7 +9,9 @@
  * reference instruction by instruction wherever the order of floating-point
  * operations is observable:
  *   - every vaddps/vmulps/vdivps/vsqrtps is one correctly rounded C operator,
- *   - every vfmadd/vfnmadd is one fmaf() call,
+ *   - every vfmadd/vfnmadd is one fmaf() call (the hardware FMA, -mfma),
+ *   - the path functions run under the reference's MXCSR FTZ+DAZ
+ *     (v7_oracle_fpenv.h), as the reference's kernels do,
  *   - the eight-lane YMM accumulators are modelled as explicit arrays and
  *     reduced by the same addition tree as the reference's HADD_YMM macro.
  * Compile with -ffp-contract=off and without -ffast-math (see Makefile).
@@ -23,6 +25,19 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+
+#include "v7_oracle_fpenv.h"
+
+static int g_ref_fp_env = 1;
+void orc_set_reference_fp_env(int on) { g_ref_fp_env = on ? 1 : 0; }
+int orc_get_reference_fp_env(void) { return g_ref_fp_env; }
+unsigned orc_fp_enter(void)
+{
+    unsigned old = _mm_getcsr();
+    if (g_ref_fp_env)
+        _mm_setcsr(old | 0x8040u); /* FTZ (bit 15) + DAZ (bit 6) */
+    return old;
+}
 
 /* ------------------------------------------------------------------------ */
 /* HADD_YMM: src/asm/v7_macros.inc:38-45.  v[i] + v[i+4] for i < 4, then
@@ -51,6 +66,7 @@ static float hadd8(const float v[8])
  * HADD_YMM (add_rmsnorm_kernel.inc:70-73, v7_macros.inc:286-289). */
 float orc_sumsq_lanes(const float *x, int n)
 {
+    ORC_REFERENCE_FP_ENV;
     float acc[4][8];
     memset(acc, 0, sizeof(acc));
     int blocks = n / 8;
@@ -78,6 +94,7 @@ float orc_sumsq_lanes(const float *x, int n)
  * rmsnorm_rope_dispatch.inc:20). */
 float orc_rms_scale(float sumsq, int n, float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     float mean = sumsq / (float)n;
     float val = mean + eps;
     float root = sqrtf(val);
@@ -90,6 +107,7 @@ float orc_rms_scale(float sumsq, int n, float eps)
  * Pass 2: o = (scale * residual) * weight, two vmulps (:87-94). */
 void orc_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int dim, float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     for (int i = 0; i < dim; ++i)
         residual[i] = residual[i] + add[i];
     float ss = orc_sumsq_lanes(residual, dim);
@@ -103,6 +121,7 @@ void orc_fused_add_rmsnorm(float *o, float *residual, const float *add, const fl
 void orc_fused_add_rmsnorm_rows(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
                                 float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     for (int r = 0; r < rows; ++r)
         orc_fused_add_rmsnorm(o + (long long)r * dim, residual + (long long)r * dim, add + (long long)r * dim, weight,
                               dim, eps);
@@ -147,6 +166,7 @@ static void rope_head(float *x, int head_dim, const float *w, const float *c, co
 void orc_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, const float *norm_weight, const float *cos_table,
                             const float *sin_table, int pos, int rope_max_dim, float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     const float *c = cos_table + (long long)pos * rope_max_dim;
     const float *s = sin_table + (long long)pos * rope_max_dim;
     for (int h = 0; h < n_heads; ++h)
@@ -157,6 +177,7 @@ void orc_rmsnorm_rope_tokens(float *buf, int n_tokens, long long token_stride, i
                              const float *norm_weight, const float *cos_table, const float *sin_table,
                              const int32_t *positions, int rope_max_dim, float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     for (int t = 0; t < n_tokens; ++t)
         orc_rmsnorm_rope_heads(buf + (long long)t * token_stride, n_heads, head_dim, norm_weight, cos_table, sin_table,
                                positions[t], rope_max_dim, eps);
@@ -247,6 +268,7 @@ static float bits_to_float(uint32_t u)
 
 float orc_sigmoid(float g)
 {
+    ORC_REFERENCE_FP_ENV;
     const float log2e = (float)1.4426950408889634; /* scalar_log2e / s_log2e_v */
     const float c5 = bits_to_float(0x3AADD303u);
     const float c4 = bits_to_float(0x3C1E7411u);
@@ -276,6 +298,7 @@ float orc_sigmoid(float g)
  * out = (sigmoid(g) * g) * u, two vmulps. */
 void orc_swiglu(float *out, const float *gate, const float *up, long long n)
 {
+    ORC_REFERENCE_FP_ENV;
     for (long long i = 0; i < n; ++i) {
         float g = gate[i];
         float sg = orc_sigmoid(g) * g;
@@ -359,6 +382,7 @@ static float group_absmax(const float *x, int gs)
 
 void orc_quantize(int8_t *out_q, const float *in_x, float *out_s, long long n, int gs)
 {
+    ORC_REFERENCE_FP_ENV;
     long long full = n / gs;
     for (long long g = 0; g < full; ++g) {
         const float *x = in_x + g * gs;
@@ -388,6 +412,7 @@ void orc_quantize(int8_t *out_q, const float *in_x, float *out_s, long long n, i
 
 void orc_quantize_rows(int8_t *out_q, const float *in_x, float *out_s, int rows, int row_len, int gs)
 {
+    ORC_REFERENCE_FP_ENV;
     int spr = (row_len + gs - 1) / gs;
     for (int r = 0; r < rows; ++r)
         orc_quantize(out_q + (long long)r * row_len, in_x + (long long)r * row_len, out_s + (long long)r * spr, row_len,
@@ -398,6 +423,7 @@ void orc_quantize_rows(int8_t *out_q, const float *in_x, float *out_s, int rows,
  * row, then v7d_quantize over the same row with n = hidden_dim). */
 void orc_swiglu_q8_rows(int8_t *out_q, float *out_s, const float *gate, const float *up, int rows, int hidden, int gs)
 {
+    ORC_REFERENCE_FP_ENV;
     float *buf = (float *)malloc((size_t)hidden * sizeof(float));
     if (!buf)
         return;
@@ -434,6 +460,7 @@ void orc_embedding_gather(float *out, const int32_t *ids, int n_tokens, int dim,
  * COMPUTE_RMS_SCALE with (float)size; phase 2 is o = (scale * x) * weight, two vmulps. */
 void orc_rmsnorm(float *o, const float *x, const float *weight, int size, float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     float ss = orc_sumsq_lanes(x, size);
     float s = orc_rms_scale(ss, size, eps);
     for (int i = 0; i < size; ++i) {
@@ -444,6 +471,7 @@ void orc_rmsnorm(float *o, const float *x, const float *weight, int size, float 
 
 void orc_rmsnorm_rows(float *o, const float *x, const float *weight, int rows, int dim, float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     for (int r = 0; r < rows; ++r)
         orc_rmsnorm(o + (long long)r * dim, x + (long long)r * dim, weight, dim, eps);
 }
@@ -458,6 +486,7 @@ void orc_rmsnorm_rows(float *o, const float *x, const float *weight, int rows, i
 void orc_rmsnorm_quantize_rows(int8_t *out_q, float *out_s, const float *x, const float *weight, int rows, int dim,
                                int gs, float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     float *buf = (float *)malloc((size_t)dim * sizeof(float));
     if (!buf)
         return;
@@ -473,6 +502,7 @@ void orc_rmsnorm_quantize_rows(int8_t *out_q, float *out_s, const float *x, cons
  * (vaddps), n % 32 == 0. */
 void orc_add_inplace(float *x, const float *y, long long n)
 {
+    ORC_REFERENCE_FP_ENV;
     for (long long i = 0; i < n; ++i)
         x[i] = x[i] + y[i];
 }
@@ -529,6 +559,7 @@ void orc_kv_pack_f16(uint16_t *dst, const float *src, long long n)
 void orc_rope_only_heads(float *buf, int n_heads, int head_dim, const float *cos_table, const float *sin_table,
                          int pos, int rope_max_dim)
 {
+    ORC_REFERENCE_FP_ENV;
     if (pos == 0)
         return;
     const float *c = cos_table + (long long)pos * rope_max_dim;
@@ -552,6 +583,7 @@ void orc_rope_only_heads(float *buf, int n_heads, int head_dim, const float *cos
  * (src/asm/prefill_q8.inc:848-879); n is all_heads_dim or kv_dim. */
 void orc_bias_add(float *x, const float *bias, long long n)
 {
+    ORC_REFERENCE_FP_ENV;
     for (long long i = 0; i < n; ++i)
         x[i] = x[i] + bias[i];
 }

@@ -7,8 +7,9 @@
  * Every function restates one reference kernel of cpki-gmbh/v7multiplikator
  * in scalar C, reproducing its operation order, rounding points and FMA
  * placement (see the per-function citations in v7_oracle.c).  Build flags:
- * -O2 -ffp-contract=off, no fast-math, so every C operator is one IEEE-754
- * binary32 operation rounded to nearest-even and fmaf() is the only fused op.
+ * -O2 -mfma -ffp-contract=off, no fast-math, so every C operator is one
+ * binary32 operation rounded to nearest-even and fmaf() is the only fused op,
+ * in the reference's MXCSR FTZ+DAZ mode (below).
  */
 #ifndef V7_ORACLE_H
 #define V7_ORACLE_H
@@ -17,6 +18,16 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* Floating-point environment.  The reference computes under MXCSR FTZ+DAZ: init ORs 0x8040 into
+ * the init thread's MXCSR (src/asm/v7_init.inc:103-108), every dispatch entry reloads that image on
+ * the calling thread (SET_FTZ_DAZ, src/asm/v7_core.inc:301-303) and the direct calls that follow on
+ * that thread inherit it.  Each path function below enters that mode (denormal inputs read as zero,
+ * results that are still tiny after rounding flushed to zero) and restores the caller's MXCSR on
+ * return; the C operators compile to the SSE scalar instructions that obey it, and fmaf() to the
+ * hardware FMA (-mfma).  orc_set_reference_fp_env(0) switches the mode off, to show what it changes. */
+void orc_set_reference_fp_env(int on);
+int orc_get_reference_fp_env(void);
 
 /* a1: v7s_fused_add_rmsnorm, one row; dim % 8 == 0 */
 void orc_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int dim, float eps);

@@ -11,6 +11,7 @@
  * src/asm/prefill_q8.inc:1159-1166, src/asm/forward.inc:13-42.
  */
 #include "v7_oracle.h"
+#include "v7_oracle_fpenv.h"
 
 #include <immintrin.h>
 #include <math.h>
@@ -56,6 +57,7 @@ static AVX2 float rms_scale(float ss, int n, float eps)
 AVX2 void orc_avx2_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int dim,
                                      float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     int blocks = dim >> 3;
     __m256 a = _mm256_setzero_ps(), b = _mm256_setzero_ps(), c = _mm256_setzero_ps(), d = _mm256_setzero_ps();
     float *r = residual;
@@ -98,6 +100,7 @@ AVX2 void orc_avx2_fused_add_rmsnorm(float *o, float *residual, const float *add
 AVX2 void orc_avx2_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, const float *w, const float *cos_table,
                                       const float *sin_table, int pos, int rope_max_dim, float eps)
 {
+    ORC_REFERENCE_FP_ENV;
     const float *ct = cos_table + (long long)pos * rope_max_dim;
     const float *st = sin_table + (long long)pos * rope_max_dim;
     int half = head_dim / 2;
@@ -166,6 +169,7 @@ static AVX2 __m256 sigmoid_ps(__m256 g)
 /* .pq_ffn_silu, prefill_q8.inc:1159-1166; n % 8 == 0 on the vector path */
 AVX2 void orc_avx2_swiglu(float *out, const float *gate, const float *up, long long n)
 {
+    ORC_REFERENCE_FP_ENV;
     long long i = 0;
     for (; i + 8 <= n; i += 8) {
         __m256 g = _mm256_loadu_ps(gate + i);
@@ -196,13 +200,14 @@ static AVX2 void quant32(int8_t *q, const float *x, __m256 recip)
 /* v7s_quantize_chunk, quantize_kernel.inc:44-159, for gs in {32, 64} */
 AVX2 void orc_avx2_quantize(int8_t *out_q, const float *in_x, float *out_s, long long n, int gs)
 {
+    ORC_REFERENCE_FP_ENV;
     const __m256 absmask = _mm256_castsi256_ps(_mm256_set1_epi32(0x7FFFFFFF));
     long long full = n / gs;
     for (long long g = 0; g < full; ++g) {
         const float *x = in_x + g * gs;
         __m256 v[8];
-        for (int j = 0; j < gs / 8; ++j)
-            v[j] = _mm256_and_ps(absmask, _mm256_loadu_ps(x + 8 * j));
+        for (int j = 0; j < 8; ++j)
+            v[j] = j < gs / 8 ? _mm256_and_ps(absmask, _mm256_loadu_ps(x + 8 * j)) : _mm256_setzero_ps();
         /* the reference's pairing (quantize_kernel.inc:62-83), which fixes where a NaN survives */
         __m256 m = _mm256_max_ps(_mm256_max_ps(v[0], v[1]), _mm256_max_ps(v[2], v[3]));
         if (gs == 64)
@@ -267,6 +272,7 @@ static void chain_rows(const orc_chain_args *a, int t0, int t1)
 
 static void *chain_thread(void *p)
 {
+    ORC_REFERENCE_FP_ENV;
     chain_job *j = (chain_job *)p;
     for (int r = 0; r < j->reps; ++r)
         chain_rows(j->a, j->t0, j->t1);

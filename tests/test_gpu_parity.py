@@ -43,9 +43,8 @@ def assert_bits(got, want, what=""):
     want = np.asarray(want)
     assert got.shape == want.shape, (what, got.shape, want.shape)
     if got.dtype.kind == "f":
-        same = (got == want) | (np.isnan(got) & np.isnan(want))
-        # +0/-0 must match too
-        same &= np.signbit(got) == np.signbit(want)
+        # +0/-0 must match too; a NaN matches any NaN (x86 makes its default NaN negative, the GPU positive)
+        same = ((got == want) & (np.signbit(got) == np.signbit(want))) | (np.isnan(got) & np.isnan(want))
     else:
         same = got == want
     if not same.all():
@@ -813,3 +812,112 @@ def test_torch_ops_reject_undersized_outputs_and_mismatched_tables(ops):
     ops.rmsnorm_rope_heads(q, qw, c, c)
     ops.fused_add_rmsnorm(r, a, w)
     torch.cuda.synchronize()
+
+
+# --------------------------------------------------------------------------- denormal data: the reference's FTZ + DAZ
+
+F = np.float32
+
+
+def denormal_mix(seed, shape):
+    """Rows of four kinds, cycled: denormals (random bits), tiny normals whose squares and products are
+    denormal (N(0,1) * 2^-66), values just above 2^-126, and ordinary N(0,1) values sprinkled with all three."""
+    rng = C.rng(seed)
+    rows = int(np.prod(shape[:-1]))
+    n = shape[-1]
+    x = np.empty((rows, n), F)
+    for r in range(rows):
+        kind = r % 4
+        if kind == 0:
+            bits = rng.integers(0, 0x00800000, n, dtype=np.uint32) | (rng.integers(0, 2, n, dtype=np.uint32) << 31)
+            x[r] = bits.view(F)
+        elif kind == 1:
+            x[r] = rng.standard_normal(n).astype(F) * F(2.0 ** -66)
+        elif kind == 2:
+            x[r] = (F(2.0 ** -126) * (1 + rng.random(n))).astype(F) * rng.choice(np.array([-1, 1], F), n)
+        else:
+            x[r] = rng.standard_normal(n).astype(F)
+            pick = rng.integers(0, n, n // 4)
+            x[r, pick] = (rng.standard_normal(pick.size) * 2.0 ** -128).astype(F)
+    return x.reshape(shape)
+
+
+@pytest.mark.parametrize("eps", [0.0, 1e-6])
+def test_denormal_rows_norms_follow_ftz_daz(ops, oracle, eps):
+    """add+RMSNorm, RMSNorm, RMSNorm->Q8 and the fused add->RMSNorm->Q8 on rows of denormals and tiny values,
+    bit for bit with the oracle in the reference's MXCSR FTZ+DAZ mode (eps = 0 lets an all-flushed sum of
+    squares give an infinite scale)."""
+    dim = 256
+    r = denormal_mix(501, (16, dim))
+    a = denormal_mix(502, (16, dim))[::-1].copy()
+    w = C.norm_weight(503, dim)
+    wo, wr = oracle.fused_add_rmsnorm(r, a, w, eps)
+    rt = dev(r)
+    o = ops.fused_add_rmsnorm(rt, dev(a), dev(w), eps=eps)
+    assert_bits(host(rt), wr, "residual")
+    assert_bits(host(o), wo, "o")
+    assert_bits(host(ops.rmsnorm(dev(r), dev(w), eps=eps)), oracle.rmsnorm(r, w, eps), "rmsnorm")
+    for gs in (32, 64):
+        q, sc = ops.rmsnorm_quantize(dev(r), dev(w), eps=eps, gs=gs)
+        wq, ws = oracle.rmsnorm_quantize(r, w, eps, gs)
+        assert_bits(host(q), wq, "codes")
+        assert_bits(host(sc), ws, "scales")
+        q, sc = ops.add_rmsnorm_quantize(dev(r), dev(a), dev(w), eps=eps, gs=gs)
+        wq, ws = oracle.rmsnorm_quantize(oracle.add_inplace(r, a), w, eps, gs)
+        assert_bits(host(q), wq, "fused codes")
+        assert_bits(host(sc), ws, "fused scales")
+
+
+def test_denormal_heads_rope_follow_ftz_daz(ops, oracle):
+    """Q/K RMSNorm+RoPE, RoPE only and the Q/K/V stage with bias on heads of denormals and tiny values."""
+    T, HQ, HK, D = 8, 8, 4, 128
+    q = denormal_mix(511, (T, HQ, D))
+    k = denormal_mix(512, (T, HK, D))
+    qw = C.norm_weight(513, D)
+    kw = C.norm_weight(514, D)
+    ct, st = oracle.rope_tables(T, D, 1e6)
+    pos = np.arange(T, dtype=np.int32)
+    qt, kt = dev(q), dev(k)
+    ops.qk_rmsnorm_rope(qt, kt, dev(qw), dev(kw), dev(ct), dev(st), positions=dev(pos), eps=1e-6)
+    assert_bits(host(qt), oracle.rmsnorm_rope(q, qw, ct, st, pos, 1e-6), "q")
+    assert_bits(host(kt), oracle.rmsnorm_rope(k, kw, ct, st, pos, 1e-6), "k")
+    bt = dev(q)
+    ops.rope_only_heads(bt, dev(ct), dev(st), positions=dev(pos))
+    assert_bits(host(bt), oracle.rope_only(q, ct, st, pos), "rope only")
+    v = denormal_mix(515, (T, HK, D))
+    qb = denormal_mix(516, (HQ * D,))
+    kb = denormal_mix(517, (HK * D,))
+    vb = denormal_mix(518, (HK * D,))
+    want = oracle.qkv_stage(q, k, v, qw, kw, qb, kb, vb, ct, st, pos, 1e-6)
+    qt, kt, vt = dev(q), dev(k), dev(v)
+    kc = torch.empty((T, HK, D), dtype=torch.float16, device="cuda")
+    vc = torch.empty((T, HK, D), dtype=torch.float16, device="cuda")
+    ops.qkv_rope_stage(qt, kt, vt, dev(ct), dev(st), positions=dev(pos), eps=1e-6, q_norm_weight=dev(qw),
+                       k_norm_weight=dev(kw), q_bias=dev(qb), k_bias=dev(kb), v_bias=dev(vb), k_cache=kc, v_cache=vc)
+    for got, exp, name in zip((host(qt), host(kt), host(vt)), want[:3], ("q", "k", "v")):
+        assert_bits(got, exp, f"stage {name}")
+    assert_bits(host(kc).view(np.uint16), oracle.kv_pack_f16(want[1].reshape(T, -1)).reshape(T, HK, D), "k cache")
+    assert_bits(host(vc).view(np.uint16), oracle.kv_pack_f16(want[2].reshape(T, -1)).reshape(T, HK, D), "v cache")
+
+
+@pytest.mark.parametrize("rows,row_len", [(32, 4096), (12, 1000)])
+def test_denormal_swiglu_and_quantize_follow_ftz_daz(ops, oracle, rows, row_len):
+    """SwiGLU, SwiGLU->Q8, Q8 quantize (flat and general paths), add and the binary16 pack on denormal data;
+    quantizer groups whose max is below 2^-118 are where a denormal element's code depends on DAZ."""
+    g = denormal_mix(521, (rows, row_len))
+    u = denormal_mix(522, (rows, row_len))[::-1].copy()
+    assert_bits(host(ops.swiglu(dev(g), dev(u))), oracle.swiglu(g, u), "swiglu")
+    x = g.copy()
+    x[1::4] = (x[1::4] * F(2.0 ** -54)).astype(F)  # group maxima near 2^-120: the floor scale meets denormals
+    for gs in (32, 64):
+        wq, ws = oracle.swiglu_q8(g, u, gs)
+        gq, gsc = ops.swiglu_q8(dev(g), dev(u), gs=gs)
+        assert_bits(host(gq), wq, "swiglu_q8 codes")
+        assert_bits(host(gsc), ws, "swiglu_q8 scales")
+        wq, ws = oracle.quantize(x, gs)
+        gq, gsc = ops.quantize_q8(dev(x), gs=gs)
+        assert_bits(host(gq), wq, "quantize codes")
+        assert_bits(host(gsc), ws, "quantize scales")
+    assert_bits(host(ops.add_inplace(dev(g), dev(u))), oracle.add_inplace(g, u), "add_inplace")
+    if row_len % 4 == 0:
+        assert_bits(host(ops.kv_pack_f16(dev(g))).view(np.uint16), oracle.kv_pack_f16(g), "kv pack")

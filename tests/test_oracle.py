@@ -552,6 +552,79 @@ def test_swiglu_q8_is_quantize_of_swiglu_and_near_double(oracle):
         assert np.max(np.abs(q.reshape(16, -1, gs) - ideal)) <= 0.5 + 1e-3
 
 
+# --------------------------------------------------------------------------- FP environment: MXCSR FTZ + DAZ
+
+avx2_early = pytest.mark.skipif("not __import__('oracle.oracle', fromlist=['x']).avx2_available()",
+                                reason="host CPU lacks AVX2/FMA")
+
+
+def test_oracle_runs_in_the_reference_fp_environment(oracle):
+    """The reference computes under MXCSR FTZ+DAZ (src/asm/v7_init.inc:103-108, SET_FTZ_DAZ
+    src/asm/v7_core.inc:301-303): a denormal input reads as zero and a result still below 2^-126 after
+    rounding becomes zero.  Hand-traced cases, each also run with gradual underflow to show the switch
+    is what decides them:
+    - quantize, x = [2^-120, 1.5*2^-127, 0...]: wmax 2^-120 is below the floor, so scale 2^-126 and
+      reciprocal 2^126; 2^-120 -> 64; the denormal reads as 0 -> code 0 (gradual underflow: 0.75 -> 1);
+    - RMSNorm, 64 x 2^-70, w = 1, eps = 0: every square 2^-140 flushes, sumsq = 0, scale = 1/sqrt(0) = Inf,
+      o = Inf (gradual underflow: sumsq 2^-134, mean 2^-140, scale 2^70, o = 1);
+    - SwiGLU, g = 2^-130, u = 1: the clamp reads g as 0, sigmoid = 1/(1+1) = 0.5, sigma*g = 0.5*0 = 0
+      (gradual underflow: 2^-131);
+    - add, 2^-127 + 2^-127 = 0 (gradual underflow: 2^-126); 1.5*2^-126 - 2^-126, two normal inputs whose
+      sum 2^-127 flushes = 0 (gradual underflow, or DAZ alone: 2^-127);
+    - RMSNorm+RoPE at pos 0 of a head of 64 x 2^-127, eps 1e-6: x reads as 0, so every output is 0
+      (gradual underflow: x * 1/sqrt(eps) is about 2^-117)."""
+    d = np.float32(2.0 ** -127) * np.float32(1.5)
+    xq = np.zeros((1, 64), F)
+    xq[0, 0] = 2.0 ** -120
+    xq[0, 1] = d
+    x70 = np.full((1, 64), 2.0 ** -70, F)
+    g = np.array([2.0 ** -130], F)
+    a = np.array([2.0 ** -127], F)
+    head = np.full((1, 1, 64), 2.0 ** -127, F)
+    ct, st = oracle.rope_tables(1, 64, 1e6)
+    pos = np.zeros(1, np.int32)
+
+    def run():
+        q, s = oracle.quantize(xq, 64)
+        return (q[0, :2].tolist(), float(s[0, 0]), float(oracle.rmsnorm(x70, np.ones(64, F), 0.0)[0, 0]),
+                float(oracle.swiglu(g, np.ones(1, F))[0]), float(oracle.add_inplace(a, a)[0]),
+                float(oracle.add_inplace(np.array([1.5 * 2.0 ** -126], F), np.array([-2.0 ** -126], F))[0]),
+                float(np.max(np.abs(oracle.rmsnorm_rope(head, np.ones(64, F), ct, st, pos, 1e-6)))))
+
+    assert oracle.lib().orc_get_reference_fp_env() == 1
+    q, s, o, sw, ad, ad2, rope = run()
+    assert q == [64, 0] and s == 2.0 ** -126
+    assert o == np.inf and sw == 0.0 and ad == 0.0 and ad2 == 0.0 and rope == 0.0
+    with oracle.gradual_underflow():
+        q, s, o, sw, ad, ad2, rope = run()
+    assert q == [64, 1] and s == 2.0 ** -126
+    assert o == 1.0 and sw == 2.0 ** -131 and ad == 2.0 ** -126 and ad2 == 2.0 ** -127 and 0 < rope < 2.0 ** -100
+    assert oracle.lib().orc_get_reference_fp_env() == 1
+
+
+@avx2_early
+def test_avx2_form_matches_scalar_oracle_on_denormal_data(oracle):
+    """Both restatements in the reference's FTZ+DAZ mode agree bit for bit on data full of denormals and
+    tiny values (the AVX2 form runs the same vector instructions as the reference)."""
+    rng = C.rng(71)
+    bits = rng.integers(0, 0x00800000, (8, 4096), dtype=np.uint32) | (rng.integers(0, 2, (8, 4096), dtype=np.uint32) << 31)
+    x = bits.view(F).copy()
+    x[:, ::3] = C.normal(72, (8, 4096))[:, ::3] * np.float32(2.0 ** -60)
+    x[:, ::7] = C.normal(73, (8, 4096))[:, ::7]
+    y = x[::-1].copy()
+    w = C.norm_weight(74, 4096)
+    assert all(bits_equal(p, q) for p, q in zip(oracle.avx2_fused_add_rmsnorm_rows(x, y, w, 0.0),
+                                                 oracle.fused_add_rmsnorm(x, y, w, 0.0)))
+    assert bits_equal(oracle.avx2_swiglu(x.reshape(-1), y.reshape(-1)), oracle.swiglu(x.reshape(-1), y.reshape(-1)))
+    for gs in (32, 64):
+        assert all(bits_equal(p, q) for p, q in zip(oracle.avx2_quantize(x, gs), oracle.quantize(x, gs)))
+    h = x.reshape(8, 32, 128)
+    ct, st = oracle.rope_tables(8, 128, 1e6)
+    pos = np.arange(8, dtype=np.int32)
+    assert bits_equal(oracle.avx2_rmsnorm_rope(h, w[:128], ct, st, pos, 1e-6),
+                      oracle.rmsnorm_rope(h, w[:128], ct, st, pos, 1e-6))
+
+
 # --------------------------------------------------------------------------- embedding dequant (a9)
 
 def test_embedding_closed_form(oracle):

@@ -4,7 +4,7 @@
 Each mutant is a mistake a restatement of the reference kernels could plausibly make: another reduction
 tree or accumulator pairing, leftover blocks taken last, an unfused FMA chain or rotation, a fused or
 reordered scale, a missing pos-0 branch, a quantizer without its floor or with another rounding, a wrong
-scale index, a truncating or flushing binary16 conversion.  The AVX2 cross-check is left out (it is a
+scale index, a truncating or flushing binary16 conversion, an FP environment with DAZ or FTZ alone.  The AVX2 cross-check is left out (it is a
 second restatement, not an independent fact), and so are the golden fixtures (written by the oracle).
 """
 from __future__ import annotations
@@ -117,6 +117,12 @@ MUTANTS = [
     ("quant: lanes i+4 first",
      "        float p0 = vmax(m[0], m[4]), p1 = vmax(m[1], m[5]), p2 = vmax(m[2], m[6]), p3 = vmax(m[3], m[7]);",
      "        float p0 = vmax(m[4], m[0]), p1 = vmax(m[5], m[1]), p2 = vmax(m[6], m[2]), p3 = vmax(m[7], m[3]);"),
+    ("fp env: DAZ without FTZ",
+     "        _mm_setcsr(old | 0x8040u); /* FTZ (bit 15) + DAZ (bit 6) */",
+     "        _mm_setcsr(old | 0x0040u);"),
+    ("fp env: FTZ without DAZ",
+     "        _mm_setcsr(old | 0x8040u); /* FTZ (bit 15) + DAZ (bit 6) */",
+     "        _mm_setcsr(old | 0x8000u);"),
     ("quant: recip from wmax",
      "        float recip = 1.0f / scale;               /* vdivss (:88) */",
      "        float recip = 127.0f / wmax;"),
@@ -182,12 +188,12 @@ MUTANTS = [
 def _run(name, a, b, orig, work):
     d = os.path.join(work, "".join(ch if ch.isalnum() else "_" for ch in name))
     os.makedirs(d)
-    for f in ("v7_oracle_avx2.c", "v7_oracle.h"):
+    for f in ("v7_oracle_avx2.c", "v7_oracle.h", "v7_oracle_fpenv.h"):
         shutil.copy(os.path.join(ORACLE, f), d)
     with open(os.path.join(d, "v7_oracle.c"), "w") as fh:
         fh.write(orig.replace(a, b))
     so = os.path.join(d, "liboracle.so")
-    subprocess.run(["gcc", "-O2", "-fPIC", "-std=gnu11", "-ffp-contract=off", "-fno-fast-math", "-shared", "-o", so,
+    subprocess.run(["gcc", "-O2", "-mfma", "-fPIC", "-std=gnu11", "-ffp-contract=off", "-fno-fast-math", "-shared", "-o", so,
                     os.path.join(d, "v7_oracle.c"), os.path.join(d, "v7_oracle_avx2.c"), "-lm", "-lpthread"],
                    check=True, capture_output=True)
     env = dict(os.environ, V7G_ORACLE_LIB=so)

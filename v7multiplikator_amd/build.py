@@ -4,6 +4,8 @@
 
 Flags: -O3, -ffp-contract=off (every a*b+c stays two roundings; the kernels
 place every fused multiply-add explicitly, as the reference places vfmadd),
+-fgpu-flush-denormals-to-zero (f32 denormals flushed on input and output, the
+reference's MXCSR FTZ+DAZ),
 packed-FP32 instructions disabled (-Xclang -target-feature -Xclang
 -packed-fp32-ops), default correctly rounded f32 division and sqrt.
 """
@@ -23,6 +25,7 @@ ARCH = os.environ.get("V7G_OFFLOAD_ARCH", "gfx950")
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+    "-fgpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]

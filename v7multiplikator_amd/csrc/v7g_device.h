@@ -1,13 +1,20 @@
 // v7g_device.h -- device-side arithmetic shared by the gfx950 kernels.
 //
 // The reference kernels are AVX2 NASM with IEEE binary32 arithmetic, round to
-// nearest-even.  Every helper below reproduces one reference instruction
-// sequence with one correctly rounded gfx950 operation per x86 operation.
-// The library is built with -ffp-contract=off, so `a * b + c` stays two
-// roundings and __builtin_fmaf is the only fused multiply-add; f32 division
-// and sqrt are the correctly rounded expansions (hipcc's default).  The hot
-// loops replace two divisions by shorter sequences that give the same bits
-// for every input they can receive (rcp_rn, div127_rn below).
+// nearest-even, under MXCSR FTZ+DAZ (src/asm/v7_init.inc:103-108,
+// SET_FTZ_DAZ src/asm/v7_core.inc:301-303): a denormal input reads as zero and
+// a result still below 2^-126 after rounding becomes zero.  The library is
+// built with f32 denormals flushed (-fgpu-flush-denormals-to-zero), which
+// gives the same results for the operations used here (add, multiply, fma,
+// division, sqrt, compare, med3, conversion to binary16); a v_cndmask select
+// passes a denormal through unflushed, which no output below can observe.
+// Every helper reproduces one reference instruction sequence with one
+// correctly rounded gfx950 operation per x86 operation.  The library is built
+// with -ffp-contract=off, so `a * b + c` stays two roundings and
+// __builtin_fmaf is the only fused multiply-add; f32 division and sqrt are
+// the correctly rounded expansions (hipcc's default).  The hot loops replace
+// two divisions by shorter sequences that give the same bits for every input
+// they can receive (rcp_rn, div127_rn below).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -31,13 +38,19 @@ __device__ __forceinline__ float rcp_rn(float d) {
 
 // x / 127 correctly rounded, for finite x >= 127*2^-126: q0 = x*RN(1/127),
 // the remainder x - 127*q0 is exact in one fma, and one more fma corrects q0.
-// Equal to the IEEE division for every such x (exhaustively checked by
+// With denormals flushed a remainder below 2^-126 (x below about 2^-103)
+// would read as zero, so x below 2^64 is divided as x*2^64 and the quotient
+// scaled back by 2^-64, both exact (powers of two, normal results).  Equal to
+// the IEEE division for every such x (exhaustively checked by
 // v7g_arith_selfcheck()).
 __device__ __forceinline__ float div127_rn(float x) {
+  const bool small = x < 0x1p64f;
+  const float xs = small ? x * 0x1p64f : x;
   const float inv = 1.0f / 127.0f;
-  float q0 = x * inv;
-  float r = __builtin_fmaf(-q0, 127.0f, x);
-  return __builtin_fmaf(r, inv, q0);
+  const float q0 = xs * inv;
+  const float r = __builtin_fmaf(-q0, 127.0f, xs);
+  const float q = __builtin_fmaf(r, inv, q0);
+  return small ? q * 0x1p-64f : q;
 }
 
 // EVAL_SIGMOID, packed form (src/asm/v7_macros.inc:98-160):
