@@ -89,6 +89,20 @@ def build_hbm_streams(verbose: bool = False) -> str:
     return exe
 
 
+def build_fp_env_probe(verbose: bool = False) -> str:
+    """Builds probe/fp_env.hip (flush-mode gfx950 arithmetic against SSE under MXCSR FTZ+DAZ) as v7g_fp_env."""
+    src = os.path.join(PKG, "probe", "fp_env.hip")
+    exe = os.path.join(PKG, "v7g_fp_env")
+    cmd = [hipcc(), *[f for f in HIP_FLAGS if f not in ("-shared", "-fPIC")], "-o", exe, src]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in l)
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")
+    return exe
+
+
 def build_test_shim(verbose: bool = False) -> str:
     """Test support: tests/libdropin_shim.so, System V wrappers of the ms_abi drop-in entries."""
     src = os.path.join(ROOT, "tests", "dropin_shim.c")
