@@ -95,6 +95,27 @@ typedef void(V7_ABI *v7s_rmsnorm_rope_heads_fn)(float *buf, int n_heads, int hea
 V7_ABI void v7s_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, float *norm_weight, float *cos_table,
                                    float *sin_table, int pos, int rope_max_dim);
 
+/* The descriptor of v7s_qk_fork_heads (src/asm/qk_fork_kernel.inc:10-28), 48 bytes: buf holds
+ * `heads` contiguous heads of head_dim floats, weight the per-head norm weight; cos and sin point at
+ * the position's table row already (the caller adds pos * rope_max_dim, src/asm/forward_q8.inc:50-71);
+ * pos only decides whether the heads rotate (pos 0: norm only). */
+typedef struct v7g_qk_fork_args {
+  float *buf;
+  float *weight;
+  float *cos;
+  float *sin;
+  int head_dim;
+  int heads;
+  int pos;
+  int unused;
+} v7g_qk_fork_args;
+
+/* Replaces v7s_qk_fork_heads (internal in v7, src/asm/qk_fork_kernel.inc:37-62): the reentrant,
+ * descriptor-driven RMSNorm+RoPE over one descriptor's heads, the form the Q8 decode step calls for
+ * Q and K concurrently (src/asm/forward_q8.inc:322-343).  Same arithmetic and contract as
+ * v7s_rmsnorm_rope_heads; eps from v7g_set_rms_eps. */
+V7_ABI void v7s_qk_fork_heads(const v7g_qk_fork_args *desc);
+
 /* Replaces v7d_quantize, typedef src/v7_lib.h:123, src/asm/utility_dispatch.inc:108-212:
  * n floats -> n int8 codes + ceil(n/64) f32 scales, group size 64. */
 typedef void(V7_ABI *v7d_quantize_fn)(char *out_q, float *in_x, float *out_s, int n);

@@ -69,3 +69,17 @@ void shim_rope_only_heads(float *buf, int n_heads, int head_dim, float *cos_tabl
 {
     v7s_rope_only_heads(buf, n_heads, head_dim, cos_table, sin_table, pos, rope_max_dim);
 }
+
+void shim_qk_fork_heads(float *buf, float *weight, float *cos_row, float *sin_row, int head_dim, int heads, int pos)
+{
+    v7g_qk_fork_args d;
+    d.buf = buf;
+    d.weight = weight;
+    d.cos = cos_row;
+    d.sin = sin_row;
+    d.head_dim = head_dim;
+    d.heads = heads;
+    d.pos = pos;
+    d.unused = 0;
+    v7s_qk_fork_heads(&d);
+}

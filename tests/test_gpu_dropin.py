@@ -43,6 +43,7 @@ def shim():
     S.shim_add_inplace.argtypes = [vp, vp, i]
     S.shim_kv_pack_f16.argtypes = [vp, vp, i]
     S.shim_rope_only_heads.argtypes = [vp, i, i, vp, vp, i, i]
+    S.shim_qk_fork_heads.argtypes = [vp, vp, vp, vp, i, i, i]
     torch.cuda.synchronize()
     L.v7g_set_stream(torch.cuda.current_stream().cuda_stream)
     L.v7g_clear_last_error()
@@ -217,3 +218,24 @@ def test_v7s_rope_only_heads_per_token(shim, oracle, heads, hd, pos):
     S.shim_rope_only_heads(bt.data_ptr(), heads, hd, ctt.data_ptr(), stt.data_ptr(), pos, hd // 2)
     done(L)
     assert bits(bt.cpu().numpy(), oracle.rope_only(buf, ct, st, np.array([pos], np.int32)))
+
+
+@pytest.mark.parametrize("heads,hd,pos,rmd", [(8, 128, 0, 64), (32, 128, 17, 64), (8, 128, 300, 96), (4, 64, 5, 32),
+                                              (2, 256, 9, 128)])
+def test_v7s_qk_fork_heads_descriptor(shim, oracle, heads, hd, pos, rmd):
+    """The descriptor form (src/asm/qk_fork_kernel.inc:10-62): cos/sin pre-offset to row pos of a table with
+    rope_max_dim floats per row (rmd >= head_dim/2), exactly what v7s_rmsnorm_rope_heads computes."""
+    S, L = shim
+    L.v7g_set_rms_eps(1e-6)
+    buf = C.normal(heads * hd + pos, (1, heads, hd))
+    w = C.norm_weight(hd + 1, hd)
+    c0, s0 = oracle.rope_tables(pos + 1, hd, 1e6)
+    ct = np.full((pos + 1, rmd), np.nan, np.float32)  # a wider table: the columns past head_dim/2 are never read
+    st = np.full((pos + 1, rmd), np.nan, np.float32)
+    ct[:, : hd // 2], st[:, : hd // 2] = c0, s0
+    bt, wt, ctt, stt = dev(buf), dev(w), dev(ct), dev(st)
+    row = pos * rmd * 4
+    S.shim_qk_fork_heads(bt.data_ptr(), wt.data_ptr(), ctt.data_ptr() + row, stt.data_ptr() + row, hd, heads, pos)
+    done(L)
+    want = oracle.rmsnorm_rope(buf, w, ct, st, np.array([pos], np.int32), 1e-6)
+    assert bits(bt.cpu().numpy(), want)

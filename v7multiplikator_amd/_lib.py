@@ -72,6 +72,7 @@ DROP_IN = [
     "v7s_rmsnorm_quantize",
     "v7s_add_inplace",
     "v7s_rmsnorm_rope_heads",
+    "v7s_qk_fork_heads",
     "v7d_quantize",
     "v7s_embedding_row",
     "v7s_swiglu_row",

@@ -674,6 +674,27 @@ V7_ABI void v7s_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, float 
                          nullptr, pos, rope_max_dim, rows_through(pos), g_eps.load());
 }
 
+V7_ABI void v7s_qk_fork_heads(const v7g_qk_fork_args *desc) {
+  if (!desc) {
+    fail(V7G_ERR_NULL);
+    return;
+  }
+  const v7g_qk_fork_args d = *desc;  // a host descriptor, as the reference's lives on its caller's stack
+  if (d.pos < 0 || d.head_dim < 64 || d.head_dim % 32 != 0) {
+    fail(V7G_ERR_SHAPE);
+    return;
+  }
+  // cos/sin already point at row pos.  Hand the kernel a table of rows of head_dim/2 floats whose row
+  // pos starts there: base = cos - pos*half, which lies inside the caller's table (its rows hold
+  // rope_max_dim >= half floats), and the kernel reads only row pos.
+  const int half = d.head_dim / 2;
+  const uintptr_t back = (uintptr_t)d.pos * (uintptr_t)half * sizeof(float);
+  const float *cos_base = d.cos ? reinterpret_cast<const float *>(reinterpret_cast<uintptr_t>(d.cos) - back) : nullptr;
+  const float *sin_base = d.sin ? reinterpret_cast<const float *>(reinterpret_cast<uintptr_t>(d.sin) - back) : nullptr;
+  v7g_rmsnorm_rope_heads(d.buf, 1, (long long)d.heads * d.head_dim, d.heads, d.head_dim, d.weight, cos_base,
+                         sin_base, nullptr, d.pos, half, rows_through(d.pos), g_eps.load());
+}
+
 V7_ABI void v7d_quantize(char *out_q, float *in_x, float *out_s, int n) {
   if (n <= 0) {
     if (n < 0) fail(V7G_ERR_SHAPE);
