@@ -13,7 +13,7 @@
 // caches (nontemporal loads: each table row is read once); the scales and the
 // output use ordinary accesses.  Ordinary stores leave the output rows in the
 // caches for the layer that reads them next; inside the per-layer chain at
-// T = 8192 they took the gather from 32.4 to 28.7 us with the same chain total
+// T = 8192 they took the gather from 31.0 to 27.7 us with the same chain total
 // as streaming stores (the lines drain while the next kernels run).  Rows of
 // any dim % 64 == 0 take ceil(dim/4096) blocks; a partial last block clamps
 // its loads and predicates its stores.
