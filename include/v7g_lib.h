@@ -271,7 +271,7 @@ int v7g_rmsnorm_quantize(int8_t *out_q, float *out_s, const float *x, const floa
 int v7g_add_rmsnorm_quantize(int8_t *out_q, float *out_s, float *residual, const float *add, const float *weight,
                              int rows, int dim, int gs, float eps);
 
-/* x[i] += y[i] for n floats (v7s_add_inplace); 16-byte aligned pointers. */
+/* x[i] += y[i] for n floats (v7s_add_inplace), 0 <= n < 2^40; 16-byte aligned pointers. */
 int v7g_add_inplace(float *x, const float *y, long long n);
 
 /* RMSNorm+RoPE over n_tokens tokens of n_heads heads each.  Token t's heads
@@ -349,7 +349,7 @@ int v7g_qk_rmsnorm_rope_kv(float *q, long long q_token_stride, int n_q_heads, co
 int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long long src_stride, int rows,
                     int row_len);
 
-/* out[i] = (sigmoid(gate[i]) * gate[i]) * up[i] for n elements; out may alias gate. */
+/* out[i] = (sigmoid(gate[i]) * gate[i]) * up[i] for n elements, 0 <= n < 2^40; out may alias gate. */
 int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n);
 
 /* SwiGLU -> Q8: rows x hidden, group size gs (32 or 64, or any 1..4096 on the

@@ -146,6 +146,8 @@ def test_quantize_and_swiglu_reject(L):
     # gs 1 over 2^38 groups would need more than 2^30 blocks on the general path
     assert _sticky(L, L.v7g_quantize_q8, FAKE, FAKE, FAKE, 1 << 20, 1 << 18, 1)[0] == 2
     assert _sticky(L, L.v7g_swiglu_f32, FAKE, FAKE, FAKE, -1)[0] == 2
+    assert _sticky(L, L.v7g_swiglu_f32, FAKE, FAKE, FAKE, 1 << 40)[0] == 2  # one float4 per thread: grid bound
+    assert _sticky(L, L.v7g_add_inplace, FAKE, FAKE, 1 << 40)[0] == 2
     assert _sticky(L, L.v7g_swiglu_f32, FAKE, FAKE + 8, FAKE, 16)[0] == 3
     assert _sticky(L, L.v7g_swiglu_f32, None, None, None, 0) == (0, 0)
 

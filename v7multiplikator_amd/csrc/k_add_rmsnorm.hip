@@ -110,16 +110,16 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
     } else {
       // QGS/4 consecutive lanes hold one group (dim % QGS == 0 and TPR % 16 == 0:
       // a group is entirely live or entirely past the row); every lane takes
-      // part in the DPP butterfly, or, in a wave holding a NaN, in the
-      // reference's ordered vmaxps tree (rmsnorm_quantize_kernel.inc:158-186).
+      // part in the DPP butterfly, or, in a wave holding a NaN or an Inf, in
+      // the reference's ordered vmaxps tree (rmsnorm_quantize_kernel.inc:158-186).
       constexpr int LPG = QGS / 4;
       float m = lane_absmax4(n);
       float scale, recip;
       uint32_t codes;
-      if (!wave_any_nan(m)) {
+      if (!wave_any_nonfinite(m)) {
         m = (LPG == 8) ? group8_max(m) : group16_max(m);
-        q8_scale(m, scale, recip);
-        codes = pack4_codes(n, recip);
+        q8_scale_finite(m, scale, recip);
+        codes = pack4_codes_finite(n, recip);
       } else {
         q8_scale(q8_floor(group_absmax_tree<QGS>(n)), scale, recip);
         codes = pack4_codes_full(n, recip);

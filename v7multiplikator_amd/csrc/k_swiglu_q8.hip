@@ -16,8 +16,8 @@
 // Vector layout: lane owns 4 consecutive floats (streaming dwordx4 loads of
 // gate and up, or x), GS/4 consecutive lanes form one group, the group max is
 // a DPP butterfly inside 8 or 16 lanes (the reference's ordered vmaxps tree in
-// a wave that holds a NaN), each lane stores its 4 codes as one dword, and the
-// first lane of the group stores the scale.  The divisions of
+// a wave that holds a NaN or an Inf), each lane stores its 4 codes as one
+// dword, and the first lane of the group stores the scale.  The divisions of
 // the reference (sigmoid's 1/(1+e), wmax/127, 1/scale) are the shorter
 // sequences of v7g_device.h that give the same bits for every reachable input.
 #include "v7g_device.h"
@@ -25,26 +25,26 @@
 
 namespace v7g {
 
-// One float4 chunk per thread and a grid that covers the array once: a
-// thread's loads are issued together and many waves keep them in flight.  The
-// grid-stride loop only runs more than once past 2^30 chunks.
+// One float4 chunk per thread and a grid that covers the array once, with no
+// loop: a thread's loads are issued together, many waves keep them in flight,
+// and a wave carries no loop or grid-stride bookkeeping (a grid-stride loop
+// cost the SwiGLU -> Q8 kernel 20 vector instructions per wave and about 2%
+// of its time).  Addresses are the block's uniform base plus a 32-bit lane
+// offset (scalar base, vector offset loads).  The element counts the entries
+// accept (below 2^40) keep the grid below 2^31 blocks.
 constexpr unsigned kStreamBlock = 256;
-constexpr long long kMaxStreamBlocks = 1ll << 22;
 
-static unsigned stream_blocks(long long n4) {
-  long long b = (n4 + kStreamBlock - 1) / kStreamBlock;
-  return (unsigned)(b < kMaxStreamBlocks ? b : kMaxStreamBlocks);
-}
+static unsigned stream_blocks(long long n4) { return (unsigned)((n4 + kStreamBlock - 1) / kStreamBlock); }
 
 __global__ __launch_bounds__(kStreamBlock) void swiglu_f32_kernel(float *out, const float *gate, const float *up,
                                                                   long long n4) {
-  const long long stride = (long long)gridDim.x * kStreamBlock;
-  for (long long c = (long long)blockIdx.x * kStreamBlock + threadIdx.x; c < n4; c += stride) {
-    const float4 g = ld_stream4(gate + 4 * c);
-    const float4 u = ld_stream4(up + 4 * c);
-    st_stream4(out + 4 * c,
-               make_float4(swiglu_v7(g.x, u.x), swiglu_v7(g.y, u.y), swiglu_v7(g.z, u.z), swiglu_v7(g.w, u.w)));
-  }
+  const long long c0 = (long long)blockIdx.x * kStreamBlock;  // the block's first chunk (uniform)
+  if (c0 + threadIdx.x >= n4) return;
+  const unsigned t4 = 4u * threadIdx.x;
+  const float4 g = ld_stream4((gate + 4 * c0) + t4);
+  const float4 u = ld_stream4((up + 4 * c0) + t4);
+  st_stream4((out + 4 * c0) + t4,
+             make_float4(swiglu_v7(g.x, u.x), swiglu_v7(g.y, u.y), swiglu_v7(g.z, u.z), swiglu_v7(g.w, u.w)));
 }
 
 // Elements n - n%4 .. n-1 (fewer than 4), one thread each.
@@ -64,12 +64,12 @@ void launch_swiglu_f32(float *out, const float *gate, const float *up, long long
 // v7s_add_inplace (src/asm/add_kernel.inc:26-49): x = x + y, one vaddps per
 // element; streamed like the kernels above.
 __global__ __launch_bounds__(kStreamBlock) void add_inplace_kernel(float *x, const float *y, long long n4) {
-  const long long stride = (long long)gridDim.x * kStreamBlock;
-  for (long long c = (long long)blockIdx.x * kStreamBlock + threadIdx.x; c < n4; c += stride) {
-    const float4 a = ld_stream4(x + 4 * c);
-    const float4 b = ld_stream4(y + 4 * c);
-    st_stream4(x + 4 * c, make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w));
-  }
+  const long long c0 = (long long)blockIdx.x * kStreamBlock;
+  if (c0 + threadIdx.x >= n4) return;
+  const unsigned t4 = 4u * threadIdx.x;
+  const float4 a = ld_stream4((x + 4 * c0) + t4);
+  const float4 b = ld_stream4((y + 4 * c0) + t4);
+  st_stream4((x + 4 * c0) + t4, make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w));
 }
 
 __global__ void add_inplace_tail_kernel(float *x, const float *y, long long start, long long n) {
@@ -95,31 +95,35 @@ __global__ __launch_bounds__(kStreamBlock) void quantize_q8_flat_kernel(int8_t *
                                                                         const float *__restrict__ gate,
                                                                         const float *__restrict__ up, long long n4) {
   constexpr int LPG = GS / 4;  // lanes per group
-  const long long stride = (long long)gridDim.x * kStreamBlock;
-  for (long long c = (long long)blockIdx.x * kStreamBlock + threadIdx.x; c < n4; c += stride) {
+  {
+    const long long c0 = (long long)blockIdx.x * kStreamBlock;  // the block's first chunk (uniform)
+    const long long c = c0 + threadIdx.x;
+    if (c >= n4) return;
+    const unsigned t4 = 4u * threadIdx.x;
     float4 v;
     if constexpr (SWIGLU) {
-      const float4 g = ld_stream4(gate + 4 * c);
-      const float4 u = ld_stream4(up + 4 * c);
+      const float4 g = ld_stream4((gate + 4 * c0) + t4);
+      const float4 u = ld_stream4((up + 4 * c0) + t4);
       v = make_float4(swiglu_v7(g.x, u.x), swiglu_v7(g.y, u.y), swiglu_v7(g.z, u.z), swiglu_v7(g.w, u.w));
     } else {
-      v = ld_stream4(x + 4 * c);
+      v = ld_stream4((x + 4 * c0) + t4);
     }
     // absmax: without NaN the vmaxps tree is a plain maximum, a DPP butterfly
-    // here; a wave holding a NaN takes the reference's ordered tree instead.
+    // here; a wave holding a NaN takes the reference's ordered tree instead,
+    // and one holding an Inf the same general path (scale Inf, codes 0 / -127).
     float m = lane_absmax4(v);
     float scale, recip;
     uint32_t codes;
-    if (!wave_any_nan(m)) {
+    if (!wave_any_nonfinite(m)) {
       m = (LPG == 8) ? group8_max(m) : group16_max(m);
-      q8_scale(m, scale, recip);
-      codes = pack4_codes(v, recip);
+      q8_scale_finite(m, scale, recip);
+      codes = pack4_codes_finite(v, recip);
     } else {
       q8_scale(q8_floor(group_absmax_tree<GS>(v)), scale, recip);
       codes = pack4_codes_full(v, recip);
     }
-    st_stream_u32(reinterpret_cast<uint32_t *>(out_q) + c, codes);
-    if ((threadIdx.x & (LPG - 1)) == 0) st_stream_f32(out_s + c / LPG, scale);
+    st_stream_u32((reinterpret_cast<uint32_t *>(out_q) + c0) + threadIdx.x, codes);
+    if ((threadIdx.x & (LPG - 1)) == 0) st_stream_f32((out_s + c0 / LPG) + threadIdx.x / LPG, scale);
   }
 }
 

@@ -412,7 +412,7 @@ int v7g_add_rmsnorm_quantize(int8_t *out_q, float *out_s, float *residual, const
 }
 
 int v7g_add_inplace(float *x, const float *y, long long n) {
-  if (n < 0) return fail(V7G_ERR_SHAPE);
+  if (n < 0 || n >= (1LL << 40)) return fail(V7G_ERR_SHAPE);  // one float4 per thread: below 2^31 blocks
   if (n == 0) return V7G_OK;
   if (!x || !y) return fail(V7G_ERR_NULL);
   if (!al16(x) || !al16(y)) return fail(V7G_ERR_ALIGN);
@@ -567,7 +567,7 @@ int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long 
 }
 
 int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n) {
-  if (n < 0) return fail(V7G_ERR_SHAPE);
+  if (n < 0 || n >= (1LL << 40)) return fail(V7G_ERR_SHAPE);  // one float4 per thread: below 2^31 blocks
   if (n == 0) return V7G_OK;
   if (!out || !gate || !up) return fail(V7G_ERR_NULL);
   if (!al16(out) || !al16(gate) || !al16(up)) return fail(V7G_ERR_ALIGN);

@@ -135,6 +135,22 @@ __device__ __forceinline__ uint32_t pack4_codes_full(float4 v, float recip) {
          (q8_code_byte_full(v.z * recip) << 16) | (q8_code_byte_full(v.w * recip) << 24);
 }
 
+
+// The fast path of a group whose lanes hold only finite values: the group max
+// is finite, so q8_scale's Inf case cannot arise and every code's v lies in
+// [-127.00003, 127.00003], where the magic-number rounding needs no clamp.
+__device__ __forceinline__ void q8_scale_finite(float wmax, float &scale, float &recip) {
+  const uint32_t wb = __builtin_bit_cast(uint32_t, wmax), fb = __builtin_bit_cast(uint32_t, V7G_Q_FLOOR);
+  scale = div127_rn(__builtin_bit_cast(float, __builtin_elementwise_max(wb, fb)));
+  recip = rcp_rn(scale);
+}
+__device__ __forceinline__ uint32_t q8_code_byte_finite(float v) {
+  return __builtin_bit_cast(uint32_t, v + 12582912.0f) & 0xffu;
+}
+__device__ __forceinline__ uint32_t pack4_codes_finite(float4 v, float recip) {
+  return q8_code_byte_finite(v.x * recip) | (q8_code_byte_finite(v.y * recip) << 8) |
+         (q8_code_byte_finite(v.z * recip) << 16) | (q8_code_byte_finite(v.w * recip) << 24);
+}
 // vmaxps / vmaxss a, b: a > b ? a : b, the second operand when either is NaN.
 __device__ __forceinline__ float vmax_x86(float a, float b) { return (a > b) ? a : b; }
 
@@ -227,8 +243,10 @@ __device__ __forceinline__ float lane_absmax4(float4 v) {
       __builtin_elementwise_maximum(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
 }
 
-// True for every lane of the wave when some lane's value is NaN.
-__device__ __forceinline__ bool wave_any_nan(float m) { return __builtin_amdgcn_ballot_w64(m != m) != 0; }
+// True for every lane of the wave when some lane's value is NaN or infinite.
+__device__ __forceinline__ bool wave_any_nonfinite(float m) {
+  return __builtin_amdgcn_ballot_w64(!(m < __builtin_inff())) != 0;
+}
 
 // One level of an ordered max tree across lanes l and l ^ MASK: the lane with
 // the bit clear supplies the first operand, so both lanes get the same value.
