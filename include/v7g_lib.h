@@ -23,6 +23,21 @@
  * v7g_set_stream (default: the null stream); v7g_sync() waits for it.  Host
  * threads may drive different streams concurrently; eps (v7g_set_rms_eps) and
  * the sticky error are process-wide, as the reference's g_rms_eps global is.
+ *
+ * Outputs live in their own memory.  Each kernel reads and writes in one pass
+ * with many workgroups in flight, so an output that shares a byte with another
+ * output or with an input would be read and written in no fixed order.  Every
+ * entry rejects such a call with V7G_ERR_ALIAS before any launch, except the
+ * exact in-place forms listed at the entry (an output equal to the input it
+ * replaces element by element).  In particular Q8 codes and scales never go
+ * over their f32 source: the reference's prefill quantizes the SwiGLU row
+ * into the retired up row (src/asm/prefill_q8.inc:1169-1180), which is safe
+ * there only because its SwiGLU pass ends before the quantizer starts; the
+ * fused SwiGLU -> Q8 kernel reads up while it writes codes.  Strided layouts
+ * (Q, K and V heads inside one fused QKV row, cache rows) are compared row
+ * against row when the strides are equal, so interleaved but disjoint
+ * arguments pass; arguments with different strides are compared by the whole
+ * byte range from their first to their last row.
  */
 #ifndef V7G_LIB_H
 #define V7G_LIB_H
@@ -50,6 +65,7 @@ extern "C" {
 #define V7G_ERR_HIP 4        /* the HIP runtime reported an error */
 #define V7G_ERR_NO_TABLES 5  /* RoPE tables requested before v7s_rope_init */
 #define V7G_ERR_ADDRESS 6    /* a pointer is not memory the current device can access (pointer checks on) */
+#define V7G_ERR_ALIAS 7      /* an output overlaps another argument */
 
 /* Q8 tensor descriptor: int8 codes + per-group f32 scales (GS = 64).
  * Same layout as v7_q8_tensor, src/v7_lib.h:52-56. */
@@ -114,6 +130,7 @@ typedef struct v7g_qk_fork_args {
  * descriptor-driven RMSNorm+RoPE over one descriptor's heads, the form the Q8 decode step calls for
  * Q and K concurrently (src/asm/forward_q8.inc:322-343).  Same arithmetic and contract as
  * v7s_rmsnorm_rope_heads; eps from v7g_set_rms_eps. */
+typedef void(V7_ABI *v7s_qk_fork_heads_fn)(const v7g_qk_fork_args *desc);
 V7_ABI void v7s_qk_fork_heads(const v7g_qk_fork_args *desc);
 
 /* Replaces v7d_quantize, typedef src/v7_lib.h:123, src/asm/utility_dispatch.inc:108-212:
@@ -135,7 +152,9 @@ V7_ABI void v7s_swiglu_row(float *gate_inout, float *up, int hidden);
 
 /* SwiGLU -> Q8 over one row, the chain of src/asm/prefill_q8.inc:1154-1183
  * (.pq_ffn_silu then v7d_quantize, group size 64), fused into one launch:
- * out_q[hidden] codes, out_s[ceil(hidden/64)] scales; gate/up are not modified. */
+ * out_q[hidden] codes, out_s[ceil(hidden/64)] scales; gate/up are not modified.
+ * out_q and out_s must not overlap gate or up (V7G_ERR_ALIAS): the reference's
+ * codes-over-the-retired-up-row layout needs its own buffer here. */
 typedef void(V7_ABI *v7s_swiglu_quantize_row_fn)(char *out_q, float *gate, float *up, float *out_s, int hidden);
 V7_ABI void v7s_swiglu_quantize_row(char *out_q, float *gate, float *up, float *out_s, int hidden);
 
@@ -249,29 +268,32 @@ int v7g_arith_selfcheck(unsigned long long *mismatches);
  * ------------------------------------------------------------------------- */
 
 /* rows x dim fused add+RMSNorm; rows contiguous (row stride = dim).
- * residual is updated in place; o may alias residual.  dim % 8 == 0, dim <= 16384,
- * pointers 16-byte aligned. */
+ * residual is updated in place; o may equal residual or add, and overlaps
+ * nothing else.  dim % 8 == 0, dim <= 16384, pointers 16-byte aligned. */
 int v7g_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
                           float eps);
 
 /* rows x dim RMSNorm (v7s_rmsnorm per row): o = rmsnorm(x) * weight; o may
- * alias x.  dim % 32 == 0, dim <= 16384, pointers 16-byte aligned. */
+ * equal x.  dim % 32 == 0, dim <= 16384, pointers 16-byte aligned. */
 int v7g_rmsnorm(float *o, const float *x, const float *weight, int rows, int dim, float eps);
 
 /* rows x dim RMSNorm -> Q8 (v7s_rmsnorm_quantize per row) with group size gs
  * (32 or 64; the reference's is 64): out_q [rows*dim] int8, out_s [rows,
- * dim/gs] f32.  dim % gs == 0, dim <= 16384. */
+ * dim/gs] f32, apart from each other and from x and weight.  dim % gs == 0,
+ * dim <= 16384. */
 int v7g_rmsnorm_quantize(int8_t *out_q, float *out_s, const float *x, const float *weight, int rows, int dim, int gs,
                          float eps);
 
 /* The Q8 decode step v7s_add_inplace(residual, add) then v7s_rmsnorm_quantize
  * (src/asm/forward_q8.inc:386-387) fused into one pass over rows x dim:
  * residual += add (in place), then RMSNorm -> Q8 of the updated residual.
+ * out_q, out_s and residual apart from each other, add and weight.
  * No reference counterpart as one call; the results equal the two calls'. */
 int v7g_add_rmsnorm_quantize(int8_t *out_q, float *out_s, float *residual, const float *add, const float *weight,
                              int rows, int dim, int gs, float eps);
 
-/* x[i] += y[i] for n floats (v7s_add_inplace), 0 <= n < 2^40; 16-byte aligned pointers. */
+/* x[i] += y[i] for n floats (v7s_add_inplace), 0 <= n < 2^40; 16-byte aligned
+ * pointers; y equal to x or apart from it. */
 int v7g_add_inplace(float *x, const float *y, long long n);
 
 /* RMSNorm+RoPE over n_tokens tokens of n_heads heads each.  Token t's heads
@@ -279,7 +301,9 @@ int v7g_add_inplace(float *x, const float *y, long long n);
  * t: positions[t] (device int32 array) or, if positions is NULL, pos0 + t.
  * Tables: table_rows rows of rope_max_dim floats (a position outside the tables
  * yields NaN heads).  head_dim % 32 == 0 in [64, 512]; n_tokens times the
- * heads per token (of every side, for the Q/K and Q/K/V forms) < 2^28. */
+ * heads per token (of every side, for the Q/K and Q/K/V forms) < 2^28.  The
+ * heads (and binary16 rows) written are apart from each other and from the
+ * weights, biases, tables (table_rows rows) and positions. */
 int v7g_rmsnorm_rope_heads(float *buf, int n_tokens, long long token_stride, int n_heads, int head_dim,
                            const float *norm_weight, const float *cos_table, const float *sin_table,
                            const int32_t *positions, int pos0, int rope_max_dim, int table_rows, float eps);
@@ -345,17 +369,20 @@ int v7g_qk_rmsnorm_rope_kv(float *q, long long q_token_stride, int n_q_heads, co
 
 /* rows x row_len binary32 -> binary16 (v7s_kv_pack_f16 per row): row r from
  * src + r*src_stride to dst + r*dst_stride (strides in elements).  row_len,
- * strides % 4 == 0; dst 8-byte, src 16-byte aligned. */
+ * strides % 4 == 0; dst 8-byte, src 16-byte aligned; dst rows apart from src rows. */
 int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long long src_stride, int rows,
                     int row_len);
 
-/* out[i] = (sigmoid(gate[i]) * gate[i]) * up[i] for n elements, 0 <= n < 2^40; out may alias gate. */
+/* out[i] = (sigmoid(gate[i]) * gate[i]) * up[i] for n elements, 0 <= n < 2^40;
+ * out may equal gate (the reference's in-place form) or up, and overlaps
+ * neither otherwise. */
 int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n);
 
 /* SwiGLU -> Q8: rows x hidden, group size gs (32 or 64, or any 1..4096 on the
  * general path); out_q [rows*hidden] int8, out_s [rows, ceil(hidden/gs)] f32
  * (4-byte aligned).  Groups never cross rows; a row's last group may be
- * partial.  rows * ceil(hidden/gs) < 2^38. */
+ * partial.  rows * ceil(hidden/gs) < 2^38.  out_q and out_s apart from each
+ * other, gate and up. */
 int v7g_swiglu_q8(int8_t *out_q, float *out_s, const float *gate, const float *up, int rows, int hidden, int gs);
 
 /* Q8 block quantization of rows x row_len floats (v7d_quantize per row),
@@ -365,7 +392,7 @@ int v7g_quantize_q8(int8_t *out_q, float *out_s, const float *x, int rows, int r
 /* Q8 embedding gather: out[t, :] = dequant(table row ids[t]) for n_tokens ids
  * (device int32).  table_q [vocab, dim] int8 (4-byte aligned), table_s
  * [vocab*dim/64] f32, out 16-byte aligned.  An id outside [0, vocab) yields a
- * zero row.  dim % 64 == 0. */
+ * zero row.  dim % 64 == 0.  out apart from ids and the table. */
 int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const int8_t *table_q,
                             const float *table_s, int dim, int vocab);
 

@@ -71,7 +71,7 @@ def test_python_binding_covers_the_plain_c_entries():
 
 
 def test_error_strings(L):
-    for code in range(0, 6):
+    for code in range(0, 8):
         assert _lib.error_string(code) not in ("", "unknown error")
     assert _lib.error_string(99) == "unknown error"
 

@@ -1,7 +1,7 @@
 """gfx950 arithmetic in the library's flush mode (f32 denormals flushed on input and output) against x86 SSE
 under MXCSR FTZ+DAZ, the reference's mode (src/asm/v7_init.inc:103-108, src/asm/v7_core.inc:301-303):
 every operation the kernels use, on 2^20 operand triples at the denormal boundary, must give the same bits
-(v7multiplikator_amd/probe/fp_env.hip, built with the library's flags)."""
+(tests/fp_env.hip, built with the library's flags as tests/v7g_fp_env)."""
 from __future__ import annotations
 
 import os
@@ -11,7 +11,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-EXE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "v7multiplikator_amd", "v7g_fp_env")
+EXE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "v7g_fp_env")
 
 
 def test_flush_mode_arithmetic_equals_sse_ftz_daz():

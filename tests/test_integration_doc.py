@@ -42,3 +42,7 @@ def test_integration_loader_compiles_and_resolves():
                         os.path.join(d, "main.c"), "-ldl"], check=True, capture_output=True, text=True)
         r = subprocess.run([exe, _lib.LIB_PATH], capture_output=True, text=True, timeout=60)
         assert r.returncode == 0 and "loaded" in r.stdout, r.stdout + r.stderr
+    # every drop-in entry the library exports is one a host can bind through this loader
+    resolved = set(re.findall(r"V7G_RESOLVE\((\w+)\)", blocks[0])) - {"name"}
+    missing = [n for n in _lib.DROP_IN if n not in resolved]
+    assert not missing, missing

@@ -18,6 +18,7 @@ V7G_ERR_ALIGN = 3
 V7G_ERR_HIP = 4
 V7G_ERR_NO_TABLES = 5
 V7G_ERR_ADDRESS = 6
+V7G_ERR_ALIAS = 7
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int

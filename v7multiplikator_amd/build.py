@@ -75,24 +75,11 @@ def build_loadtest(verbose: bool = False) -> str:
     return exe
 
 
-def build_hbm_streams(verbose: bool = False) -> str:
-    """Builds probe/hbm_streams.hip, the streaming-kernel HBM ceilings by access mix, as v7g_hbm_streams."""
-    src = os.path.join(PKG, "probe", "hbm_streams.hip")
-    exe = os.path.join(PKG, "v7g_hbm_streams")
-    cmd = [hipcc(), *[f for f in HIP_FLAGS if f not in ("-shared", "-fPIC")], "-o", exe, src]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in l)
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")
-    return exe
-
-
 def build_fp_env_probe(verbose: bool = False) -> str:
-    """Builds probe/fp_env.hip (flush-mode gfx950 arithmetic against SSE under MXCSR FTZ+DAZ) as v7g_fp_env."""
-    src = os.path.join(PKG, "probe", "fp_env.hip")
-    exe = os.path.join(PKG, "v7g_fp_env")
+    """Test support: tests/fp_env.hip (flush-mode gfx950 arithmetic against SSE under MXCSR FTZ+DAZ), built
+    with the library's flags as tests/v7g_fp_env."""
+    src = os.path.join(ROOT, "tests", "fp_env.hip")
+    exe = os.path.join(ROOT, "tests", "v7g_fp_env")
     cmd = [hipcc(), *[f for f in HIP_FLAGS if f not in ("-shared", "-fPIC")], "-o", exe, src]
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -17,6 +17,7 @@
 #include <thread>
 #include <vector>
 
+#include "v7g_alias.h"
 #include "v7g_internal.h"
 #include "../../include/v7g_lib.h"
 
@@ -98,11 +99,34 @@ int check_ptrs(std::initializer_list<const void *> ps) {
   return V7G_OK;
 }
 
+// V7G_ERR_ALIAS if an output shares a byte with another output or with an
+// input (v7g_alias.h).  Entries that accept an exact in-place form leave the
+// coinciding pair out of the lists.
+int check_alias(std::initializer_list<v7g::Span> outs, std::initializer_list<v7g::Span> ins) {
+  for (auto o = outs.begin(); o != outs.end(); ++o) {
+    for (auto p = o + 1; p != outs.end(); ++p)
+      if (v7g::spans_overlap(*o, *p)) return V7G_ERR_ALIAS;
+    for (const v7g::Span &i : ins)
+      if (v7g::spans_overlap(*o, i)) return V7G_ERR_ALIAS;
+  }
+  return V7G_OK;
+}
+
+bool overlap(const v7g::Span &a, const v7g::Span &b) { return v7g::spans_overlap(a, b); }
+
 int check_add_rmsnorm(const float *o, const float *residual, const float *add, const float *weight, int rows, int dim) {
   if (rows < 0 || dim <= 0 || dim % 8 != 0 || dim > kMaxNormDim) return V7G_ERR_SHAPE;
   if (rows == 0) return V7G_OK;  // nothing to touch: empty tensors may carry NULL pointers
   if (!o || !residual || !add || !weight) return V7G_ERR_NULL;
   if (!al16(o) || !al16(residual) || !al16(add) || !al16(weight)) return V7G_ERR_ALIGN;
+  // o may be residual (the row ends as o, as in the reference) or add (read
+  // before o is written, and only by the row's own workgroup); nothing else overlaps.
+  const long long bytes = (long long)rows * dim * 4;
+  const v7g::Span O = v7g::flat_span(o, bytes), R = v7g::flat_span(residual, bytes), A = v7g::flat_span(add, bytes),
+                  W = v7g::flat_span(weight, (long long)dim * 4);
+  if ((o != residual && overlap(O, R)) || (o != add && overlap(O, A)) || overlap(R, A) || overlap(O, W) ||
+      overlap(R, W))
+    return V7G_ERR_ALIAS;
   return V7G_OK;
 }
 
@@ -130,6 +154,39 @@ int check_rope_side(const float *buf, long long token_stride, int n_heads, int h
   if (n_tokens == 0) return V7G_OK;
   if (!buf || !w) return V7G_ERR_NULL;
   if (!al16(buf) || !al16(w)) return V7G_ERR_ALIGN;
+  return V7G_OK;
+}
+
+// The head stage's arguments: a side's f32 heads are updated in place (an
+// output when written back, else an input), its binary16 rows are outputs;
+// norm weights, biases, tables and positions are inputs.  Sides inside one
+// fused QKV row share the token stride and pass when their heads are apart.
+int check_rope_alias(const v7g::RopeSide *sides, int n_sides, int n_tokens, int head_dim, const float *cos_table,
+                     const float *sin_table, const int32_t *positions, int rope_max_dim, int table_rows) {
+  v7g::Span outs[6], ins[12];
+  int no = 0, ni = 0;
+  for (int i = 0; i < n_sides; ++i) {
+    const v7g::RopeSide &sd = sides[i];
+    const long long hb = (long long)sd.n_heads * head_dim;
+    const v7g::Span f = v7g::row_span(sd.buf, n_tokens, sd.token_stride * 4, hb * 4);
+    if (!sd.cache || sd.keep_f32)
+      outs[no++] = f;
+    else
+      ins[ni++] = f;
+    if (sd.cache) outs[no++] = v7g::row_span(sd.cache, n_tokens, sd.cache_stride * 2, hb * 2);
+    ins[ni++] = v7g::flat_span(sd.norm_weight, (long long)head_dim * 4);
+    ins[ni++] = v7g::flat_span(sd.bias, hb * 4);
+  }
+  const long long table_bytes = (long long)table_rows * rope_max_dim * 4;
+  ins[ni++] = v7g::flat_span(cos_table, table_bytes);
+  ins[ni++] = v7g::flat_span(sin_table, table_bytes);
+  ins[ni++] = v7g::flat_span(positions, (long long)n_tokens * 4);
+  for (int a = 0; a < no; ++a) {
+    for (int b = a + 1; b < no; ++b)
+      if (overlap(outs[a], outs[b])) return V7G_ERR_ALIAS;
+    for (int b = 0; b < ni; ++b)
+      if (overlap(outs[a], ins[b])) return V7G_ERR_ALIAS;
+  }
   return V7G_OK;
 }
 
@@ -195,6 +252,11 @@ int check_table_shape(int n_pos, int head_dim) {
   return (n_pos <= 0 || n_pos > kRopeMaxPositions || head_dim < 2 || head_dim % 2 != 0 || head_dim > 1024)
              ? V7G_ERR_SHAPE
              : V7G_OK;
+}
+
+int check_tables_apart(const float *cos_table, const float *sin_table, int n_pos, int head_dim) {
+  const long long bytes = (long long)n_pos * (head_dim / 2) * 4;
+  return overlap(v7g::flat_span(cos_table, bytes), v7g::flat_span(sin_table, bytes)) ? V7G_ERR_ALIAS : V7G_OK;
 }
 
 int check_llama3(float factor, float low_freq_factor, float high_freq_factor, int orig_max_pos) {
@@ -301,6 +363,7 @@ const char *v7g_error_string(int code) {
     case V7G_ERR_HIP: return "the HIP runtime reported an error";
     case V7G_ERR_NO_TABLES: return "RoPE tables requested before v7s_rope_init";
     case V7G_ERR_ADDRESS: return "a pointer is not memory the current device can access";
+    case V7G_ERR_ALIAS: return "an output overlaps another argument";
     default: return "unknown error";
   }
 }
@@ -308,6 +371,7 @@ const char *v7g_error_string(int code) {
 int v7g_build_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base) {
   if (!cos_table || !sin_table) return fail(V7G_ERR_NULL);
   if (int rc = check_table_shape(n_pos, head_dim)) return fail(rc);
+  if (int rc = check_tables_apart(cos_table, sin_table, n_pos, head_dim)) return fail(rc);
   std::vector<float> c, s;
   fill_tables(c, s, n_pos, plain_freqs(head_dim / 2, rope_base));
   const int rc = copy_tables(cos_table, sin_table, c, s);
@@ -319,6 +383,7 @@ int v7g_build_rope_tables_llama3(float *cos_table, float *sin_table, int n_pos, 
   if (!cos_table || !sin_table) return fail(V7G_ERR_NULL);
   if (int rc = check_table_shape(n_pos, head_dim)) return fail(rc);
   if (int rc = check_llama3(factor, low_freq_factor, high_freq_factor, orig_max_pos)) return fail(rc);
+  if (int rc = check_tables_apart(cos_table, sin_table, n_pos, head_dim)) return fail(rc);
   std::vector<float> c, s;
   fill_tables(c, s, n_pos,
               llama3_freqs(head_dim / 2, rope_base, factor, low_freq_factor, high_freq_factor, orig_max_pos));
@@ -375,6 +440,12 @@ int v7g_rmsnorm(float *o, const float *x, const float *weight, int rows, int dim
   if (rows == 0) return V7G_OK;
   if (!o || !x || !weight) return fail(V7G_ERR_NULL);
   if (!al16(o) || !al16(x) || !al16(weight)) return fail(V7G_ERR_ALIGN);
+  {
+    const long long bytes = (long long)rows * dim * 4;
+    const v7g::Span O = v7g::flat_span(o, bytes), X = v7g::flat_span(x, bytes),
+                    W = v7g::flat_span(weight, (long long)dim * 4);
+    if ((o != x && overlap(O, X)) || overlap(O, W)) return fail(V7G_ERR_ALIAS);  // o == x: in place
+  }
   if (int pc = check_ptrs({o, x, weight})) return fail(pc);
   v7g::launch_rmsnorm(o, x, weight, rows, dim, eps, stream());
   return check_launch();
@@ -389,9 +460,20 @@ static int check_norm_q8(const int8_t *out_q, const float *out_s, const float *x
   return V7G_OK;
 }
 
+// Codes and scales beside x (and add, for the fused form), never over them.
+static int check_norm_q8_alias(const int8_t *out_q, const float *out_s, const float *x, const float *add,
+                               const float *weight, int rows, int dim, int gs) {
+  const long long n = (long long)rows * dim;
+  const v7g::Span Q = v7g::flat_span(out_q, n), S = v7g::flat_span(out_s, n / gs * 4), X = v7g::flat_span(x, n * 4),
+                  A = v7g::flat_span(add, n * 4), W = v7g::flat_span(weight, (long long)dim * 4);
+  if (add) return check_alias({Q, S, X}, {A, W});  // the residual x is updated in place: an output
+  return check_alias({Q, S}, {X, W});
+}
+
 int v7g_rmsnorm_quantize(int8_t *out_q, float *out_s, const float *x, const float *weight, int rows, int dim, int gs,
                          float eps) {
   int rc = check_norm_q8(out_q, out_s, x, weight, rows, dim, gs);
+  if (!rc && rows > 0) rc = check_norm_q8_alias(out_q, out_s, x, nullptr, weight, rows, dim, gs);
   if (rc) return fail(rc);
   if (rows == 0) return V7G_OK;
   if (int pc = check_ptrs({out_q, out_s, x, weight})) return fail(pc);
@@ -404,6 +486,7 @@ int v7g_add_rmsnorm_quantize(int8_t *out_q, float *out_s, float *residual, const
   int rc = check_norm_q8(out_q, out_s, residual, weight, rows, dim, gs);
   if (!rc && rows > 0 && !add) rc = V7G_ERR_NULL;
   if (!rc && rows > 0 && !al16(add)) rc = V7G_ERR_ALIGN;
+  if (!rc && rows > 0) rc = check_norm_q8_alias(out_q, out_s, residual, add, weight, rows, dim, gs);
   if (rc) return fail(rc);
   if (rows == 0) return V7G_OK;
   if (int pc = check_ptrs({out_q, out_s, residual, add, weight})) return fail(pc);
@@ -416,6 +499,7 @@ int v7g_add_inplace(float *x, const float *y, long long n) {
   if (n == 0) return V7G_OK;
   if (!x || !y) return fail(V7G_ERR_NULL);
   if (!al16(x) || !al16(y)) return fail(V7G_ERR_ALIGN);
+  if (x != y && overlap(v7g::flat_span(x, n * 4), v7g::flat_span(y, n * 4))) return fail(V7G_ERR_ALIAS);
   if (int pc = check_ptrs({x, y})) return fail(pc);
   v7g::launch_add_inplace(x, y, n, stream());
   return check_launch();
@@ -430,8 +514,11 @@ int v7g_rmsnorm_rope_heads(float *buf, int n_tokens, long long token_stride, int
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
-  if (int pc = check_ptrs({buf, norm_weight, cos_table, sin_table, positions})) return fail(pc);
   v7g::RopeSide side{buf, token_stride, n_heads, norm_weight};
+  if (int ac = check_rope_alias(&side, 1, n_tokens, head_dim, cos_table, sin_table, positions, rope_max_dim,
+                                table_rows))
+    return fail(ac);
+  if (int pc = check_ptrs({buf, norm_weight, cos_table, sin_table, positions})) return fail(pc);
   v7g::launch_rmsnorm_rope(&side, 1, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
                            table_rows, eps, stream());
   return check_launch();
@@ -448,9 +535,12 @@ int v7g_qk_rmsnorm_rope(float *q, long long q_token_stride, int n_q_heads, const
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
-  if (int pc = check_ptrs({q, q_norm_weight, k, k_norm_weight, cos_table, sin_table, positions})) return fail(pc);
   v7g::RopeSide sides[2] = {{q, q_token_stride, n_q_heads, q_norm_weight},
                             {k, k_token_stride, n_kv_heads, k_norm_weight}};
+  if (int ac = check_rope_alias(sides, 2, n_tokens, head_dim, cos_table, sin_table, positions, rope_max_dim,
+                                table_rows))
+    return fail(ac);
+  if (int pc = check_ptrs({q, q_norm_weight, k, k_norm_weight, cos_table, sin_table, positions})) return fail(pc);
   v7g::launch_rmsnorm_rope(sides, 2, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
                            table_rows, eps, stream());
   return check_launch();
@@ -506,11 +596,6 @@ int v7g_qkv_rope_stage(const v7g_qkv_stage *st) {
   if (!rc && st->positions && ((uintptr_t)st->positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (st->n_tokens == 0) return V7G_OK;
-  if (int pc = check_ptrs({st->q.buf, st->q.norm_weight, st->q.bias, st->k.buf, st->k.norm_weight, st->k.bias,
-                           st->k.cache, st->cos_table, st->sin_table, st->positions}))
-    return fail(pc);
-  if (has_v)
-    if (int pc = check_ptrs({st->v.buf, st->v.bias, st->v.cache})) return fail(pc);
   v7g::RopeSide sides[3];
   const v7g_qkv_side *src[3] = {&st->q, &st->k, &st->v};
   for (int i = 0; i < 3; ++i) {
@@ -524,6 +609,14 @@ int v7g_qkv_rope_stage(const v7g_qkv_stage *st) {
     sides[i].keep_f32 = src[i]->keep_f32 != 0;
     sides[i].rotate = i < 2;
   }
+  if (int ac = check_rope_alias(sides, has_v ? 3 : 2, st->n_tokens, st->head_dim, st->cos_table, st->sin_table,
+                                st->positions, st->rope_max_dim, st->table_rows))
+    return fail(ac);
+  if (int pc = check_ptrs({st->q.buf, st->q.norm_weight, st->q.bias, st->k.buf, st->k.norm_weight, st->k.bias,
+                           st->k.cache, st->cos_table, st->sin_table, st->positions}))
+    return fail(pc);
+  if (has_v)
+    if (int pc = check_ptrs({st->v.buf, st->v.bias, st->v.cache})) return fail(pc);
   v7g::launch_rmsnorm_rope(sides, has_v ? 3 : 2, st->n_tokens, st->head_dim, st->cos_table, st->sin_table,
                            st->positions, st->pos0, st->rope_max_dim, st->table_rows, st->eps, stream());
   return check_launch();
@@ -545,8 +638,11 @@ int v7g_rope_only_heads(float *buf, int n_tokens, long long token_stride, int n_
   if (!rc && positions && ((uintptr_t)positions & 3u)) rc = V7G_ERR_ALIGN;
   if (rc) return fail(rc);
   if (n_tokens == 0) return V7G_OK;
-  if (int pc = check_ptrs({buf, cos_table, sin_table, positions})) return fail(pc);
   v7g::RopeSide side{buf, token_stride, n_heads, nullptr};
+  if (int ac = check_rope_alias(&side, 1, n_tokens, head_dim, cos_table, sin_table, positions, rope_max_dim,
+                                table_rows))
+    return fail(ac);
+  if (int pc = check_ptrs({buf, cos_table, sin_table, positions})) return fail(pc);
   v7g::launch_rmsnorm_rope(&side, 1, n_tokens, head_dim, cos_table, sin_table, positions, pos0, rope_max_dim,
                            table_rows, 0.0f, stream());
   return check_launch();
@@ -561,6 +657,9 @@ int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long 
   if (rows == 0) return V7G_OK;
   if (!dst || !src) return fail(V7G_ERR_NULL);
   if (((uintptr_t)dst & 7u) || !al16(src)) return fail(V7G_ERR_ALIGN);
+  if (overlap(v7g::row_span(dst, rows, dst_stride * 2, (long long)row_len * 2),
+              v7g::row_span(src, rows, src_stride * 4, (long long)row_len * 4)))
+    return fail(V7G_ERR_ALIAS);
   if (int pc = check_ptrs({dst, src})) return fail(pc);
   v7g::launch_kv_pack_f16(dst, dst_stride, src, src_stride, rows, row_len, stream());
   return check_launch();
@@ -571,6 +670,12 @@ int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n) 
   if (n == 0) return V7G_OK;
   if (!out || !gate || !up) return fail(V7G_ERR_NULL);
   if (!al16(out) || !al16(gate) || !al16(up)) return fail(V7G_ERR_ALIGN);
+  {
+    // out == gate (the reference's in-place form) or out == up: each element is read before it is replaced
+    const v7g::Span O = v7g::flat_span(out, n * 4);
+    if ((out != gate && overlap(O, v7g::flat_span(gate, n * 4))) || (out != up && overlap(O, v7g::flat_span(up, n * 4))))
+      return fail(V7G_ERR_ALIAS);
+  }
   if (int pc = check_ptrs({out, gate, up})) return fail(pc);
   v7g::launch_swiglu_f32(out, gate, up, n, stream());
   return check_launch();
@@ -587,9 +692,20 @@ static int check_quant(const int8_t *out_q, const float *out_s, int rows, int ro
   return V7G_OK;
 }
 
+// Codes and scales in their own buffers: never over the inputs (the reference
+// writes the SwiGLU row's codes into the retired up row, src/asm/prefill_q8.inc:1169-1180,
+// after the SwiGLU pass has finished; the fused kernel reads up while it writes codes).
+static int check_quant_alias(const int8_t *out_q, const float *out_s, const float *a, const float *b, int rows,
+                             int row_len, int gs) {
+  const long long n = (long long)rows * row_len, groups = (long long)rows * ((row_len + gs - 1) / gs);
+  return check_alias({v7g::flat_span(out_q, n), v7g::flat_span(out_s, groups * 4)},
+                     {v7g::flat_span(a, n * 4), v7g::flat_span(b, n * 4)});
+}
+
 int v7g_swiglu_q8(int8_t *out_q, float *out_s, const float *gate, const float *up, int rows, int hidden, int gs) {
   int rc = check_quant(out_q, out_s, rows, hidden, gs);
   if (!rc && rows > 0 && (!gate || !up)) rc = V7G_ERR_NULL;
+  if (!rc && rows > 0) rc = check_quant_alias(out_q, out_s, gate, up, rows, hidden, gs);
   if (rc) return fail(rc);
   if (rows == 0) return V7G_OK;
   if (int pc = check_ptrs({out_q, out_s, gate, up})) return fail(pc);
@@ -600,6 +716,7 @@ int v7g_swiglu_q8(int8_t *out_q, float *out_s, const float *gate, const float *u
 int v7g_quantize_q8(int8_t *out_q, float *out_s, const float *x, int rows, int row_len, int gs) {
   int rc = check_quant(out_q, out_s, rows, row_len, gs);
   if (!rc && rows > 0 && !x) rc = V7G_ERR_NULL;
+  if (!rc && rows > 0) rc = check_quant_alias(out_q, out_s, x, nullptr, rows, row_len, gs);
   if (rc) return fail(rc);
   if (rows == 0) return V7G_OK;
   if (int pc = check_ptrs({out_q, out_s, x})) return fail(pc);
@@ -616,6 +733,13 @@ int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const 
   if ((long long)n_tokens * ((dim / 4 + 1023) / 1024) >= (1LL << 24)) return fail(V7G_ERR_SHAPE);
   if (!al16(out) || ((uintptr_t)table_q & 3u) || ((uintptr_t)table_s & 3u) || ((uintptr_t)ids & 3u))
     return fail(V7G_ERR_ALIGN);
+  {
+    const long long cells = (long long)vocab * dim;
+    if (check_alias({v7g::flat_span(out, (long long)n_tokens * dim * 4)},
+                    {v7g::flat_span(ids, (long long)n_tokens * 4), v7g::flat_span(table_q, cells),
+                     v7g::flat_span(table_s, cells / 64 * 4)}))
+      return fail(V7G_ERR_ALIAS);
+  }
   if (int pc = check_ptrs({out, ids, table_q, table_s})) return fail(pc);
   v7g::launch_embedding_gather(out, ids, n_tokens, table_q, table_s, dim, vocab, stream());
   return check_launch();
@@ -719,6 +843,11 @@ V7_ABI void v7s_embedding_row(float *out, int token, int dim, v7g_q8_tensor *q_d
   const float *s = q_desc->s + (base >> 6);
   if (!al16(out) || ((uintptr_t)q & 3u) || ((uintptr_t)s & 3u)) {
     fail(V7G_ERR_ALIGN);
+    return;
+  }
+  if (check_alias({v7g::flat_span(out, (long long)dim * 4)},
+                  {v7g::flat_span(q, dim), v7g::flat_span(s, (long long)dim / 64 * 4)})) {
+    fail(V7G_ERR_ALIAS);
     return;
   }
   if (int pc = check_ptrs({out, q, s})) {
