@@ -263,6 +263,18 @@ int v7g_rope_init_llama3(int head_dim, float rope_base, int n_pos, float factor,
  * No reference counterpart. */
 int v7g_arith_selfcheck(unsigned long long *mismatches);
 
+/* v7g_arith_selfcheck without allocating: no counterpart in the reference;
+ * for callers that cannot allocate device memory (serving loops and harnesses
+ * that forbid hipMalloc, e.g. a periodic device health check between
+ * batches).  Bit w of `checks` (1..15) selects identity w; mismatches[w] is
+ * written for the selected identities only, with the value
+ * v7g_arith_selfcheck gives.  The counts live in 32 bytes of static device
+ * memory, one copy per device, kept until the process ends; the entry makes
+ * no allocation.  Calls that overlap on one device share those counters and
+ * race: serialise them.  Synchronous.  V7G_ERR_SHAPE for checks outside
+ * 1..15 (there are four identities, four counters). */
+int v7g_arith_selfcheck_noalloc(unsigned long long *mismatches, int checks);
+
 /* ---------------------------------------------------------------------------
  * 3. Batched entries (performance path)
  * ------------------------------------------------------------------------- */

@@ -11,6 +11,7 @@
 // Each case walks its whole range of bit patterns (about 2^31, 2^31, 2^32 and
 // 2^32 values), a few milliseconds of GPU time.  Results are per-block counts in
 // caller-visible device memory, summed on the host.
+#include <mutex>
 #include <vector>
 
 #include "v7g_device.h"
@@ -65,9 +66,8 @@ __device__ __forceinline__ uint32_t f16_bits_sw(float f) {
 constexpr int kCheckBlocks = 4096;
 constexpr int kChecks = 4;
 
-__global__ __launch_bounds__(256) void arith_check_kernel(int which, uint64_t lo, uint64_t count,
-                                                          unsigned long long *block_counts) {
-  __shared__ unsigned long long part[256];
+// Mismatches of identity `which` among this thread's share of patterns lo .. lo+count-1.
+__device__ __forceinline__ unsigned long long count_mismatches(int which, uint64_t lo, uint64_t count) {
   unsigned long long bad = 0;
   const uint64_t stride = (uint64_t)gridDim.x * 256u;
   for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < count; i += stride) {
@@ -94,23 +94,50 @@ __global__ __launch_bounds__(256) void arith_check_kernel(int which, uint64_t lo
     }
     bad += __builtin_bit_cast(uint32_t, fast) != __builtin_bit_cast(uint32_t, exact);
   }
+  return bad;
+}
+
+// The workgroup's total (every thread must call it).
+__device__ __forceinline__ unsigned long long block_total(unsigned long long bad) {
+  __shared__ unsigned long long part[256];
   part[threadIdx.x] = bad;
   __syncthreads();
   for (int h = 128; h > 0; h >>= 1) {
     if (threadIdx.x < h) part[threadIdx.x] += part[threadIdx.x + h];
     __syncthreads();
   }
-  if (threadIdx.x == 0) block_counts[blockIdx.x] = part[0];
+  return part[0];
 }
 
+// One count per workgroup in block_counts[blockIdx.x].
+__global__ __launch_bounds__(256) void arith_check_kernel(int which, uint64_t lo, uint64_t count,
+                                                          unsigned long long *block_counts) {
+  const unsigned long long total = block_total(count_mismatches(which, lo, count));
+  if (threadIdx.x == 0) block_counts[blockIdx.x] = total;
+}
+
+// Every workgroup adds its count to *counter (cleared by the caller first).
+__global__ __launch_bounds__(256) void arith_count_kernel(int which, uint64_t lo, uint64_t count,
+                                                          unsigned long long *counter) {
+  const unsigned long long total = block_total(count_mismatches(which, lo, count));
+  if (threadIdx.x == 0 && total) atomicAdd(counter, total);
+}
+
+__global__ void clear_counters_kernel(unsigned long long *c, int n) {
+  if ((int)threadIdx.x < n) c[threadIdx.x] = 0;
+}
+
+struct CheckRange {
+  uint64_t lo, hi;
+};
+// The patterns of each identity.
+constexpr CheckRange kRanges[kChecks] = {{0x00800000ull, 0x7D000000ull},    // [2^-126, 2^123)
+                                         {0x03FE0000ull, 0x7F800000ull},    // [127*2^-126, Inf)
+                                         {0x00000000ull, 0x100000000ull},   // every pattern (NaNs skipped)
+                                         {0x00000000ull, 0x100000000ull}};  // every pattern
+
 int arith_selfcheck(unsigned long long mismatches[4], hipStream_t stream) {
-  struct Range {
-    uint64_t lo, hi;
-  };
-  const Range ranges[kChecks] = {{0x00800000ull, 0x7D000000ull},    // [2^-126, 2^123)
-                                 {0x03FE0000ull, 0x7F800000ull},    // [127*2^-126, Inf)
-                                 {0x00000000ull, 0x100000000ull},   // every pattern (NaNs skipped)
-                                 {0x00000000ull, 0x100000000ull}};  // every pattern
+  const CheckRange *ranges = kRanges;
   unsigned long long *d = nullptr;
   if (hipMalloc(&d, sizeof(unsigned long long) * kCheckBlocks * kChecks) != hipSuccess) return -1;
   for (int w = 0; w < kChecks; ++w)
@@ -130,6 +157,51 @@ int arith_selfcheck(unsigned long long mismatches[4], hipStream_t stream) {
     for (int b = 0; b < kCheckBlocks; ++b) t += h[(size_t)w * kCheckBlocks + b];
     mismatches[w] = t;
   }
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// The non-allocating form: the four counters live in `scratch`, a file-scope
+// device array (32 bytes; each device holds its own copy until the process
+// ends).  Host code never passes the array's name to a kernel: on the host it
+// is a stand-in, not a device address.  The device address comes from
+// hipGetSymbolAddress, called once per device with that device current, on the
+// entry's first call there.  Every call on a device shares its counters and
+// clears them first: calls that overlap on one device race.
+static __device__ __align__(256) unsigned long long scratch[kChecks];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static unsigned long long *g_scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch`, or nullptr on a HIP error.
+static unsigned long long *scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_scratch_ptr[dev] = static_cast<unsigned long long *>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+int arith_selfcheck_noalloc(unsigned long long mismatches[4], int checks, hipStream_t stream) {
+  unsigned long long *counters = scratch_on_current_device();
+  if (!counters) return -1;
+  enqueue(clear_counters_kernel, dim3(1), dim3(64), 0, stream, counters, kChecks);
+  for (int w = 0; w < kChecks; ++w)
+    if (checks & (1 << w))
+      enqueue(arith_count_kernel, dim3(kCheckBlocks), dim3(256), 0, stream, w, kRanges[w].lo,
+              kRanges[w].hi - kRanges[w].lo, counters + w);
+  unsigned long long h[kChecks] = {0, 0, 0, 0};
+  if (hipGetLastError() != hipSuccess ||
+      hipMemcpyAsync(h, counters, sizeof(h), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    return -1;
+  for (int w = 0; w < kChecks; ++w)
+    if (checks & (1 << w)) mismatches[w] = h[w];
   return 0;
 }
 

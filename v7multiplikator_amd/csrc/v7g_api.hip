@@ -413,6 +413,14 @@ int v7g_arith_selfcheck(unsigned long long *mismatches) {
   return rc == 0 ? V7G_OK : fail(V7G_ERR_HIP);
 }
 
+int v7g_arith_selfcheck_noalloc(unsigned long long *mismatches, int checks) {
+  if (!mismatches) return fail(V7G_ERR_NULL);
+  if (checks <= 0 || checks > 0xF) return fail(V7G_ERR_SHAPE);  // four identities, four counters
+  const int rc = v7g::arith_selfcheck_noalloc(mismatches, checks, stream());
+  v7g::launch_events() = v7g::LaunchEvents{};
+  return rc == 0 ? V7G_OK : fail(V7G_ERR_HIP);
+}
+
 int v7g_get_rope_tables(float **cos_table, float **sin_table, int *rope_max_dim, int *n_pos) {
   std::lock_guard<std::mutex> lk(g_rope_mu);
   if (!g_rope_cos) return fail(V7G_ERR_NO_TABLES);

@@ -79,5 +79,10 @@ void launch_quantize_q8(int8_t *out_q, float *out_s, const float *x, const float
 // mismatches[i] = number of inputs where identity i fails; returns 0 or -1 on
 // a HIP error.
 int arith_selfcheck(unsigned long long mismatches[4], hipStream_t stream);
+// The same identities (bit w of `checks` selects identity w) counted in the
+// library's static device counters instead of an allocated buffer; writes
+// mismatches[w] for the selected identities only.  Synchronous; returns 0 or
+// -1 on a HIP error.
+int arith_selfcheck_noalloc(unsigned long long mismatches[4], int checks, hipStream_t stream);
 
 }  // namespace v7g
