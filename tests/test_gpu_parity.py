@@ -361,6 +361,37 @@ def test_rmsnorm_quantize_nan_columns(ops, oracle, gs):
 
 
 @pytest.mark.parametrize("gs", [32, 64])
+@pytest.mark.parametrize("dim", [544, 4096, 12288])
+def test_rmsnorm_quantize_nan_at_every_group_position(ops, oracle, gs, dim):
+    """A NaN weight at each position of a quantization group in turn (group g: position g % gs), beside a
+    weight of 2^20 two positions on, through the 16-elements-per-thread kernel (dims 544: a partial wave of
+    34 threads, GS 32 only; 4096; 12288): the reference's ordered vmaxps tree keeps the NaN or drops it with
+    its partners (src/asm/rmsnorm_quantize_kernel.inc:158-187).  Also with the residual add fused in front."""
+    if dim % gs:
+        pytest.skip("dim must be a multiple of the group size")
+    rows = 3
+    groups = dim // gs
+    x = C.normal(95 + dim, (rows, dim))
+    w = C.norm_weight(96 + dim, dim)
+    g = np.arange(groups)
+    w[g * gs + g % gs] = np.nan
+    w[g * gs + (g + 2) % gs] = np.float32(2.0 ** 20)
+    wq, ws = oracle.rmsnorm_quantize(x, w, 1e-6, gs)
+    q, s = ops.rmsnorm_quantize(dev(x), dev(w), eps=1e-6, gs=gs)
+    assert_bits(host(q), wq, "codes")
+    assert_bits(host(s), ws, "scales")
+    r = C.normal(97 + dim, (rows, dim))
+    a = C.normal(98 + dim, (rows, dim))
+    r_new = oracle.add_inplace(r, a)
+    wq, ws = oracle.rmsnorm_quantize(r_new, w, 1e-6, gs)
+    rt = dev(r)
+    q, s = ops.add_rmsnorm_quantize(rt, dev(a), dev(w), eps=1e-6, gs=gs)
+    assert_bits(host(rt), r_new, "residual")
+    assert_bits(host(q), wq, "fused codes")
+    assert_bits(host(s), ws, "fused scales")
+
+
+@pytest.mark.parametrize("gs", [32, 64])
 @pytest.mark.parametrize("rows,hidden", [(1, 64), (3, 192), (16, 8192), (5, 96)])
 def test_swiglu_q8_shapes(ops, oracle, gs, rows, hidden):
     # hidden 96 with gs 64: each row ends in a 32-element tail group, quantized on its own as the
@@ -400,8 +431,10 @@ def test_rmsnorm_rows(ops, oracle, dim, seed):
 
 
 @pytest.mark.parametrize("gs", [64, 32])
-@pytest.mark.parametrize("dim", [64, 128, 512, 1024, 2048, 3072, 4096, 8192, 16384])
+@pytest.mark.parametrize("dim", [64, 128, 512, 544, 1024, 2048, 2560, 3072, 4096, 5120, 8192, 12288, 16384])
 def test_rmsnorm_quantize_rows(ops, oracle, gs, dim):
+    if dim % gs:
+        pytest.skip("dim must be a multiple of the group size")
     rows = 7
     x = C.normal(dim + gs, (rows, dim))
     w = C.norm_weight(dim, dim)
@@ -412,7 +445,7 @@ def test_rmsnorm_quantize_rows(ops, oracle, gs, dim):
 
 
 @pytest.mark.parametrize("gs", [64, 32])
-@pytest.mark.parametrize("dim", [64, 2048, 4096])
+@pytest.mark.parametrize("dim", [64, 2048, 2560, 4096, 12288])
 def test_add_rmsnorm_quantize_equals_the_two_calls(ops, oracle, gs, dim):
     """The fused decode step equals v7s_add_inplace then v7s_rmsnorm_quantize (src/asm/forward_q8.inc:386-387)."""
     rows = 9
@@ -843,11 +876,11 @@ def denormal_mix(seed, shape):
 
 
 @pytest.mark.parametrize("eps", [0.0, 1e-6])
-def test_denormal_rows_norms_follow_ftz_daz(ops, oracle, eps):
+@pytest.mark.parametrize("dim", [256, 4096])
+def test_denormal_rows_norms_follow_ftz_daz(ops, oracle, eps, dim):
     """add+RMSNorm, RMSNorm, RMSNorm->Q8 and the fused add->RMSNorm->Q8 on rows of denormals and tiny values,
     bit for bit with the oracle in the reference's MXCSR FTZ+DAZ mode (eps = 0 lets an all-flushed sum of
-    squares give an infinite scale)."""
-    dim = 256
+    squares give an infinite scale).  dim 4096 takes the 16-elements-per-thread RMSNorm->Q8 kernel."""
     r = denormal_mix(501, (16, dim))
     a = denormal_mix(502, (16, dim))[::-1].copy()
     w = C.norm_weight(503, dim)

@@ -279,6 +279,28 @@ __device__ __forceinline__ float group_absmax_tree(float4 v) {
   return vmax_x86(vmax_x86(a[0], a[2]), vmax_x86(a[1], a[3]));
 }
 
+// The same tree when each lane of the group holds 16 consecutive elements
+// (YMM vectors 2L and 2L+1 of the group on lane L; GS/16 lanes per group,
+// aligned in the wave): vectors 2L, 2L+1 pair inside the lane, the next
+// levels pair lanes L^1 (and L^2 for 64), lower lane first; then lanes i with
+// i+4 of the 8-float vector (vextractf128), k with k+2 (vmovhlps), 0 with 1
+// (vmovshdup).  Every lane of the group returns the value.
+template <int GS>
+__device__ __forceinline__ float group_absmax_tree16(const float (&a)[16]) {
+  float m[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m[i] = vmax_x86(__builtin_fabsf(a[i]), __builtin_fabsf(a[8 + i]));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    m[i] = tree_max_step<1>(m[i]);
+    if constexpr (GS == 64) m[i] = tree_max_step<2>(m[i]);
+  }
+  float r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = vmax_x86(m[i], m[i + 4]);
+  return vmax_x86(vmax_x86(r[0], r[2]), vmax_x86(r[1], r[3]));
+}
+
 // COMPUTE_RMS_SCALE, src/asm/v7_macros.inc:348-354: 1 / sqrt(sumsq/n + eps),
 // four correctly rounded operations.
 __device__ __forceinline__ float rms_scale(float sumsq, float n, float eps) {
