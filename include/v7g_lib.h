@@ -385,6 +385,17 @@ int v7g_qk_rmsnorm_rope_kv(float *q, long long q_token_stride, int n_q_heads, co
 int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long long src_stride, int rows,
                     int row_len);
 
+/* The K and V rows of a token batch packed to their binary16 cache rows in
+ * one launch: the two v7s_kv_pack_f16 calls per token of
+ * src/asm/forward_q8.inc:345-358 (src/asm/prefill_q8.inc:157-171).  Token
+ * r's K row of row_len floats at k_src + r*src_stride goes to k_dst +
+ * r*k_dst_stride, its V row at v_src + r*src_stride to v_dst +
+ * r*v_dst_stride (strides in elements: K and V of a fused QKV row share the
+ * token stride).  row_len and strides % 4 == 0; destinations 8-byte, sources
+ * 16-byte aligned; the two caches apart from each other and from the sources. */
+int v7g_kv_pack_f16_kv(uint16_t *k_dst, long long k_dst_stride, uint16_t *v_dst, long long v_dst_stride,
+                       const float *k_src, const float *v_src, long long src_stride, int rows, int row_len);
+
 /* out[i] = (sigmoid(gate[i]) * gate[i]) * up[i] for n elements, 0 <= n < 2^40;
  * out may equal gate (the reference's in-place form) or up, and overlaps
  * neither otherwise. */

@@ -177,6 +177,19 @@ def test_rope_table_builders_reject(L):
     assert _sticky(L, L.v7g_rope_init_llama3, 128, f(5e5), 16, f(8), f(1), f(0.5), 8192)[0] == 2
 
 
+def test_kv_pack_kv_rejects(L):
+    f = L.v7g_kv_pack_f16_kv
+    assert _sticky(L, f, FAKE, 1024, FAKE + (1 << 20), 1024, FAKE + (2 << 20), FAKE + (3 << 20), 6144, 4, 1022)[0] == 2
+    assert _sticky(L, f, FAKE, 1020, FAKE + (1 << 20), 1024, FAKE + (2 << 20), FAKE + (3 << 20), 6144, 4, 1024)[0] == 2
+    assert _sticky(L, f, FAKE, 1024, FAKE + (1 << 20), 1024, FAKE + (2 << 20), FAKE + (3 << 20), 512, 4, 1024)[0] == 2
+    assert _sticky(L, f, FAKE, 1024, None, 1024, FAKE + (2 << 20), FAKE + (3 << 20), 6144, 4, 1024)[0] == 1
+    assert _sticky(L, f, FAKE + 4, 1024, FAKE + (1 << 20), 1024, FAKE + (2 << 20), FAKE + (3 << 20), 6144, 4,
+                   1024)[0] == 3
+    assert _sticky(L, f, FAKE, 1024, FAKE + (1 << 20), 1024, FAKE + (2 << 20) + 8, FAKE + (3 << 20), 6144, 4,
+                   1024)[0] == 3
+    assert _sticky(L, f, None, 1024, None, 1024, None, None, 6144, 0, 1024) == (0, 0)
+
+
 def test_embedding_rejects(L):
     assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE, FAKE, 100, 1000)[0] == 2  # dim % 64
     assert _sticky(L, L.v7g_embedding_gather_q8, FAKE, FAKE, 4, FAKE, FAKE, 128, 0)[0] == 2

@@ -151,6 +151,12 @@ def test_kv_pack_embedding_and_tables_apart(L):
     # dst rows interleaved with src rows of the same byte stride, sharing one byte range
     assert _rc(L, L.v7g_kv_pack_f16, src + row_len * 4 - 8, 2 * (2 * row_len), src, 2 * row_len, rows,
                row_len) == ALIAS
+    # the one-launch K/V form: V cache over the K cache, K cache over the V source rows
+    kc, vc = BASE + (4 << 20), BASE + (5 << 20)
+    assert _rc(L, L.v7g_kv_pack_f16_kv, kc, row_len, kc + 512, row_len, src, src + row_len * 4, 3 * row_len, rows,
+               row_len) == ALIAS
+    assert _rc(L, L.v7g_kv_pack_f16_kv, src + row_len * 4 + 8, 6 * row_len, vc, row_len, src, src + row_len * 4,
+               3 * row_len, rows, row_len) == ALIAS
     ids, tq, ts = BASE + (1 << 20), BASE + (2 << 20), BASE + (3 << 20)
     assert _rc(L, L.v7g_embedding_gather_q8, tq + 4096, ids, 4, tq, ts, 128, 100) == ALIAS
     assert _rc(L, L.v7g_embedding_gather_q8, ts, ids, 4, tq, ts, 128, 100) == ALIAS

@@ -509,6 +509,25 @@ def test_kv_pack_f16_rows_strided(ops, oracle, rows, row_len, src_stride, dst_st
     assert not got[:, row_len:].any()
 
 
+@pytest.mark.parametrize("rows,kv_dim,q_dim,cache_stride", [(1, 8, 32, 8), (37, 1024, 4096, 1024),
+                                                             (8192, 1024, 4096, 1024), (9, 1284, 2048, 1300),
+                                                             (3, 4100, 0, 4104)])
+def test_kv_pack_f16_kv_one_launch(ops, oracle, rows, kv_dim, q_dim, cache_stride):
+    """K and V rows of fused QKV rows [Q | K | V] into two binary16 caches in one launch, each equal to its own
+    v7s_kv_pack_f16 (rows of 1284 and 4100 floats: partial last blocks, more than one block per row)."""
+    qkv = C.normal(rows + kv_dim, (rows, q_dim + 2 * kv_dim), 2.0)
+    d = dev(qkv)
+    kc = torch.zeros((rows, cache_stride), dtype=torch.float16, device="cuda")
+    vc = torch.zeros((rows, cache_stride), dtype=torch.float16, device="cuda")
+    ops.kv_pack_f16_kv(d[:, q_dim:q_dim + kv_dim], d[:, q_dim + kv_dim:], k_out=kc[:, :kv_dim], v_out=vc[:, :kv_dim])
+    k = host(kc).view(np.uint16)
+    v = host(vc).view(np.uint16)
+    assert_bits(k[:, :kv_dim], oracle.kv_pack_f16(qkv[:, q_dim:q_dim + kv_dim]), "K rows")
+    assert_bits(v[:, :kv_dim], oracle.kv_pack_f16(qkv[:, q_dim + kv_dim:]), "V rows")
+    assert not k[:, kv_dim:].any() and not v[:, kv_dim:].any()
+    assert np.array_equal(host(d), qkv)
+
+
 @pytest.mark.parametrize("keep", [True, False])
 @pytest.mark.parametrize("hd", [128, 96])
 def test_qk_rope_with_fused_k_pack(ops, oracle, keep, hd):

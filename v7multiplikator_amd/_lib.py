@@ -59,6 +59,7 @@ SIGNATURES = {
     "v7g_qk_rmsnorm_rope_kv": (_i, [_vp, _ll, _i, _vp, _vp, _ll, _i, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _i, _f,
                                     _vp, _ll, _i]),
     "v7g_kv_pack_f16": (_i, [_vp, _ll, _vp, _ll, _i, _i]),
+    "v7g_kv_pack_f16_kv": (_i, [_vp, _ll, _vp, _ll, _vp, _vp, _ll, _i, _i]),
     "v7g_rope_only_heads": (_i, [_vp, _i, _ll, _i, _i, _vp, _vp, _vp, _i, _i, _i]),
     "v7g_qkv_rope_stage": (_i, [_vp]),
     "v7g_swiglu_f32": (_i, [_vp, _vp, _vp, _ll]),

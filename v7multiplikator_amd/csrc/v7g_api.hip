@@ -673,6 +673,31 @@ int v7g_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long 
   return check_launch();
 }
 
+int v7g_kv_pack_f16_kv(uint16_t *k_dst, long long k_dst_stride, uint16_t *v_dst, long long v_dst_stride,
+                       const float *k_src, const float *v_src, long long src_stride, int rows, int row_len) {
+  if (rows < 0 || row_len <= 0 || row_len % 4 != 0 || k_dst_stride % 4 != 0 || v_dst_stride % 4 != 0 ||
+      src_stride % 4 != 0)
+    return fail(V7G_ERR_SHAPE);
+  if (rows > 1 && (k_dst_stride < row_len || v_dst_stride < row_len || src_stride < row_len))
+    return fail(V7G_ERR_SHAPE);
+  if ((long long)rows * (row_len / 4) >= (1LL << 32) - 256) return fail(V7G_ERR_SHAPE);
+  if (rows == 0) return V7G_OK;
+  if (!k_dst || !v_dst || !k_src || !v_src) return fail(V7G_ERR_NULL);
+  if (((uintptr_t)k_dst & 7u) || ((uintptr_t)v_dst & 7u) || !al16(k_src) || !al16(v_src)) return fail(V7G_ERR_ALIGN);
+  {
+    const long long rb = (long long)row_len;
+    const v7g::Span K = v7g::row_span(k_dst, rows, k_dst_stride * 2, rb * 2),
+                    V = v7g::row_span(v_dst, rows, v_dst_stride * 2, rb * 2);
+    if (check_alias({K, V}, {v7g::row_span(k_src, rows, src_stride * 4, rb * 4),
+                             v7g::row_span(v_src, rows, src_stride * 4, rb * 4)}))
+      return fail(V7G_ERR_ALIAS);
+  }
+  if (int pc = check_ptrs({k_dst, v_dst, k_src, v_src})) return fail(pc);
+  v7g::launch_kv_pack2_f16(k_dst, k_dst_stride, v_dst, v_dst_stride, k_src, v_src, src_stride, rows, row_len,
+                           stream());
+  return check_launch();
+}
+
 int v7g_swiglu_f32(float *out, const float *gate, const float *up, long long n) {
   if (n < 0 || n >= (1LL << 40)) return fail(V7G_ERR_SHAPE);  // one float4 per thread: below 2^31 blocks
   if (n == 0) return V7G_OK;

@@ -64,6 +64,10 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
 // binary32 -> binary16 rows (v7s_kv_pack_f16): rows x row_len (row_len % 4 == 0).
 void launch_kv_pack_f16(uint16_t *dst, long long dst_stride, const float *src, long long src_stride, int rows,
                         int row_len, hipStream_t stream);
+// The K and V rows of `rows` tokens (sharing src_stride) to two binary16 caches in one launch.
+void launch_kv_pack2_f16(uint16_t *k_dst, long long k_dst_stride, uint16_t *v_dst, long long v_dst_stride,
+                         const float *k_src, const float *v_src, long long src_stride, int rows, int row_len,
+                         hipStream_t stream);
 
 void launch_swiglu_f32(float *out, const float *gate, const float *up, long long n, hipStream_t stream);
 

@@ -11,7 +11,8 @@
 //   v7g_loadtest <libv7g.so> embedding <tokens> <vocab> <dim>
 //   v7g_loadtest <libv7g.so> rmsnorm_quantize <rows> <dim> [gs]
 //   v7g_loadtest <libv7g.so> add_rmsnorm_quantize <rows> <dim> [gs]
-//   v7g_loadtest <libv7g.so> kv_pack <tokens> <kv_dim>
+//   v7g_loadtest <libv7g.so> kv_pack <tokens> <kv_dim>       (two launches, one per side)
+//   v7g_loadtest <libv7g.so> kv_pack_kv <tokens> <kv_dim>    (K and V in one launch)
 //   v7g_loadtest <libv7g.so> qkv_stage <tokens> <q_heads> <kv_heads> <head_dim>
 //   v7g_loadtest <libv7g.so> configs          (every benchmark configuration below)
 //   v7g_loadtest <libv7g.so> next             (the widened rows at the Qwen3-8B T=8192 shape)
@@ -72,6 +73,8 @@ struct Lib {
   int (*rmsnorm_quantize)(int8_t *, float *, const float *, const float *, int, int, int, float);
   int (*add_rmsnorm_quantize)(int8_t *, float *, float *, const float *, const float *, int, int, int, float);
   int (*kv_pack_f16)(uint16_t *, long long, const float *, long long, int, int);
+  int (*kv_pack_f16_kv)(uint16_t *, long long, uint16_t *, long long, const float *, const float *, long long, int,
+                        int);
   int (*qkv_rope_stage)(const v7g_qkv_stage *);
   v7s_fused_add_rmsnorm_fn v7s_fused_add_rmsnorm;
   v7s_rmsnorm_rope_heads_fn v7s_rmsnorm_rope_heads;
@@ -110,6 +113,7 @@ int load(const char *path, Lib &L) {
   resolve(L, L.rmsnorm_quantize, "v7g_rmsnorm_quantize");
   resolve(L, L.add_rmsnorm_quantize, "v7g_add_rmsnorm_quantize");
   resolve(L, L.kv_pack_f16, "v7g_kv_pack_f16");
+  resolve(L, L.kv_pack_f16_kv, "v7g_kv_pack_f16_kv");
   resolve(L, L.qkv_rope_stage, "v7g_qkv_rope_stage");
   resolve(L, L.v7s_fused_add_rmsnorm, "v7s_fused_add_rmsnorm");
   resolve(L, L.v7s_rmsnorm_rope_heads, "v7s_rmsnorm_rope_heads");
@@ -426,8 +430,9 @@ void run_norm_q8(const Lib &L, hipStream_t st, int rows, int dim, int gs, bool a
   HIPCHECK(hipFree(w));
 }
 
-// K and V rows of a fused QKV row packed to two binary16 cache buffers.
-void run_kv_pack(const Lib &L, hipStream_t st, int T, int kv_dim, const Opts &opt) {
+// K and V rows of a fused QKV row packed to two binary16 cache buffers: two
+// v7g_kv_pack_f16 launches (one per side), or one v7g_kv_pack_f16_kv launch.
+void run_kv_pack(const Lib &L, hipStream_t st, int T, int kv_dim, bool one_launch, const Opts &opt) {
   const long long ts = 6LL * kv_dim;  // a QKV row of Qwen3-8B shape: Q = 4 kv_dim, K, V
   const double bytes = 2.0 * T * kv_dim * 4 + 2.0 * T * kv_dim * 2;
   const int sets = sets_for(bytes, opt.rotate);
@@ -441,12 +446,17 @@ void run_kv_pack(const Lib &L, hipStream_t st, int T, int kv_dim, const Opts &op
   }
   int iters = 0;
   const double us = time_calls(L, st, sets, opt, [&](int s) {
-    L.kv_pack_f16(kc[s], kv_dim, qkv[s] + 4LL * kv_dim, ts, T, kv_dim);
-    L.kv_pack_f16(vc[s], kv_dim, qkv[s] + 5LL * kv_dim, ts, T, kv_dim);
+    if (one_launch) {
+      L.kv_pack_f16_kv(kc[s], kv_dim, vc[s], kv_dim, qkv[s] + 4LL * kv_dim, qkv[s] + 5LL * kv_dim, ts, T, kv_dim);
+    } else {
+      L.kv_pack_f16(kc[s], kv_dim, qkv[s] + 4LL * kv_dim, ts, T, kv_dim);
+      L.kv_pack_f16(vc[s], kv_dim, qkv[s] + 5LL * kv_dim, ts, T, kv_dim);
+    }
   }, &iters);
   char shape[96];
-  snprintf(shape, sizeof shape, "tokens=%d kv_dim=%d (K and V, two launches)", T, kv_dim);
-  report("kv_pack_f16", shape, iters, us, bytes, sets);
+  snprintf(shape, sizeof shape, "tokens=%d kv_dim=%d (K and V, %s)", T, kv_dim,
+           one_launch ? "one launch" : "two launches");
+  report(one_launch ? "kv_pack_f16_kv" : "kv_pack_f16", shape, iters, us, bytes, sets);
   for (int s = 0; s < sets; ++s) {
     HIPCHECK(hipFree(qkv[s]));
     HIPCHECK(hipFree(kc[s]));
@@ -568,14 +578,17 @@ int main(int argc, char **argv) {
   else if (k == "add_rmsnorm_quantize" && pos.size() >= 3)
     run_norm_q8(L, st, num(1, 0), num(2, 0), num(3, 64), true, opt);
   else if (k == "kv_pack" && pos.size() >= 3)
-    run_kv_pack(L, st, num(1, 0), num(2, 0), opt);
+    run_kv_pack(L, st, num(1, 0), num(2, 0), false, opt);
+  else if (k == "kv_pack_kv" && pos.size() >= 3)
+    run_kv_pack(L, st, num(1, 0), num(2, 0), true, opt);
   else if (k == "qkv_stage" && pos.size() >= 5)
     run_qkv_stage(L, st, num(1, 0), num(2, 0), num(3, 0), num(4, 0), opt);
   else if (k == "next") {
     // The widened rows at the Qwen3-8B T=8192 shape (dim 4096, 32 Q / 8 KV heads of 128).
     run_norm_q8(L, st, 8192, 4096, 64, false, opt);
     run_norm_q8(L, st, 8192, 4096, 64, true, opt);
-    run_kv_pack(L, st, 8192, 1024, opt);
+    run_kv_pack(L, st, 8192, 1024, false, opt);
+    run_kv_pack(L, st, 8192, 1024, true, opt);
     run_qkv_stage(L, st, 8192, 32, 8, 128, opt);
   } else if (k == "configs") {
     // The benchmark configurations: C1 .. C4, then the four kernels of the

@@ -20,6 +20,7 @@ library the first call raises.
   rope_tables        <- v7s_rope_init           (src/asm/fused_dispatch.inc:58-76; Llama 3 scaling
                                                   src/asm/fused_f32_kernel.inc:149-256)
   kv_pack_f16        <- v7s_kv_pack_f16         (src/asm/kv_f16c.inc:12-52)
+  kv_pack_f16_kv     <- v7s_kv_pack_f16 for K then V (src/asm/forward_q8.inc:345-358), one launch
   rope_only_heads    <- v7s_rope_only_heads     (src/asm/rope_only_dispatch.inc:11-47)
   qkv_rope_stage     <- the per-token Q/K/V stage of the prefill, one launch (src/asm/prefill_q8.inc:848-883)
 """
@@ -387,6 +388,30 @@ def kv_pack_f16(src: torch.Tensor, out: torch.Tensor | None = None) -> torch.Ten
     rc = _lib.load().v7g_kv_pack_f16(out.data_ptr(), out.stride(0), src.data_ptr(), src.stride(0), rows, n)
     _lib.check(rc, "kv_pack_f16")
     return out
+
+
+def kv_pack_f16_kv(k_src: torch.Tensor, v_src: torch.Tensor, k_out: torch.Tensor | None = None,
+                   v_out: torch.Tensor | None = None):
+    """binary16 copies of the K and V rows [rows, row_len] (views into one fused QKV buffer: the same row
+    stride) in one launch; returns (k_out, v_out)."""
+    _need(k_src, torch.float32, "k_src", contiguous=False)
+    _need(v_src, torch.float32, "v_src", contiguous=False)
+    if k_src.dim() != 2 or k_src.stride(1) != 1 or v_src.shape != k_src.shape or v_src.stride() != k_src.stride():
+        raise ValueError("k_src and v_src must be [rows, row_len] with contiguous rows and the same row stride")
+    rows, n = k_src.shape
+    outs = []
+    for o in (k_out, v_out):
+        if o is None:
+            o = torch.empty((rows, n), dtype=torch.float16, device=k_src.device)
+        _need(o, torch.float16, "out", contiguous=False)
+        if o.shape != k_src.shape or o.stride(1) != 1:
+            raise ValueError("outputs must be [rows, row_len] with contiguous rows")
+        outs.append(o)
+    _bind(k_src)
+    rc = _lib.load().v7g_kv_pack_f16_kv(outs[0].data_ptr(), outs[0].stride(0), outs[1].data_ptr(), outs[1].stride(0),
+                                        k_src.data_ptr(), v_src.data_ptr(), k_src.stride(0), rows, n)
+    _lib.check(rc, "kv_pack_f16_kv")
+    return outs[0], outs[1]
 
 
 def rope_tables(n_pos: int, head_dim: int, rope_base: float, device="cuda", llama3: dict | None = None):
