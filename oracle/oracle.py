@@ -46,6 +46,7 @@ def lib():
             "orc_rmsnorm_rope_tokens": (None, [_f32p, c_int, c_ll, c_int, c_int, _f32p, _f32p, _f32p, _i32p, c_int,
                                                c_float]),
             "orc_rope_tables": (None, [_f32p, _f32p, c_int, c_int, c_float]),
+            "orc_rope_freqs": (None, [np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS"), c_int, c_float]),
             "orc_rope_freqs_llama3": (None, [np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS"), c_int,
                                              c_float, c_float, c_float, c_float, c_int]),
             "orc_rope_tables_llama3": (None, [_f32p, _f32p, c_int, c_int, c_float, c_float, c_float, c_float,
@@ -138,6 +139,12 @@ def rope_tables(n_pos, head_dim, base):
     s = np.empty((n_pos, half), np.float32)
     lib().orc_rope_tables(c, s, n_pos, head_dim, float(base))
     return c, s
+
+
+def rope_freqs(half, base):
+    f = np.empty(half, np.float64)
+    lib().orc_rope_freqs(f, half, float(base))
+    return f
 
 
 def rope_freqs_llama3(half, base, factor, low_freq_factor, high_freq_factor, orig_max_pos):

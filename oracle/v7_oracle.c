@@ -183,25 +183,94 @@ void orc_rmsnorm_rope_tokens(float *buf, int n_tokens, long long token_stride, i
                                positions[t], rope_max_dim, eps);
 }
 
-/* RoPE tables: src/asm/fused_f32_kernel.inc:69-147,257-303 (plain, type 0).
- * freq_j = base^(-j/half) computed in x87 extended precision and stored as a
- * double; angle = freq_j * pos in extended precision; cos/sin by fsincos,
- * rounded to float on store.  Restated with long double powl/cosl/sinl.  The
- * tables are inputs to the kernels, identical on both sides of every parity
- * check, so they need no bit parity with the x87 sequence. */
+/* The reference builds its RoPE tables with x87 instructions under control
+ * word 0x037F (64-bit significand, round to nearest, exceptions masked;
+ * src/asm/fused_f32_kernel.inc:109-110,176-177).  The same instructions, one
+ * for one, give the same bits: each helper below is one of them. */
+static long double x87_fyl2x(long double x, long double y) /* y * log2(x) */
+{
+    long double r;
+    __asm__("fyl2x" : "=t"(r) : "0"(x), "u"(y) : "st(1)");
+    return r;
+}
+static long double x87_frndint(long double x)
+{
+    long double r;
+    __asm__("frndint" : "=t"(r) : "0"(x));
+    return r;
+}
+static long double x87_f2xm1(long double x) /* 2^x - 1, |x| <= 1 */
+{
+    long double r;
+    __asm__("f2xm1" : "=t"(r) : "0"(x));
+    return r;
+}
+static long double x87_fscale(long double x, long double e) /* x * 2^trunc(e) */
+{
+    long double r;
+    __asm__("fscale" : "=t"(r) : "0"(x), "u"(e));
+    return r;
+}
+static void x87_fsincos(long double a, long double *c, long double *s)
+{
+    long double cc, ss;
+    __asm__("fsincos" : "=t"(cc), "=u"(ss) : "0"(a));
+    *c = cc;
+    *s = ss;
+}
+static unsigned short x87_enter(void)
+{
+    unsigned short old, cw = 0x037F;
+    __asm__ volatile("fnstcw %0" : "=m"(old));
+    __asm__ volatile("fldcw %0" : : "m"(cw));
+    return old;
+}
+static void x87_leave(unsigned short old) { __asm__ volatile("fldcw %0" : : "m"(old)); }
+
+/* RBIT_CALC_INV_FREQ, src/asm/fused_f32_kernel.inc:117-134: t = j/half (fdivp),
+ * y = -t * log2(base) (fchs, fyl2x), i = frndint(y), f = y - i, freq =
+ * (f2xm1(f) + 1) * 2^i (fld1, faddp, fscale); extended precision throughout. */
+static long double ref_inv_freq(float base, int j, int half)
+{
+    const long double t = (long double)j / (long double)half;
+    const long double y = x87_fyl2x((long double)base, -t);
+    const long double i = x87_frndint(y);
+    return x87_fscale(x87_f2xm1(y - i) + 1.0L, i);
+}
+
+/* Plain frequencies (rope type 0, :120-147): freq_j = RBIT_CALC_INV_FREQ
+ * stored as a double (fstp qword). */
+void orc_rope_freqs(double *freq, int half, float base)
+{
+    const unsigned short cw = x87_enter();
+    for (int j = 0; j < half; ++j) freq[j] = (double)ref_inv_freq(base, j, half);
+    x87_leave(cw);
+}
+
+/* Tables from precomputed frequencies, the .rbit_outer / .rbit_inner fill
+ * (:257-303): angle = freq_j * pos (fld qword freq, fmul qword pos: the
+ * product in extended precision), fsincos, each result rounded to float on
+ * store (fstp dword). */
+static void rope_fill(float *cos_table, float *sin_table, int n_pos, int half, const double *freq)
+{
+    const unsigned short cw = x87_enter();
+    for (int p = 0; p < n_pos; ++p)
+        for (int j = 0; j < half; ++j) {
+            long double c, s;
+            x87_fsincos((long double)freq[j] * (long double)(double)p, &c, &s);
+            cos_table[(long long)p * half + j] = (float)c;
+            sin_table[(long long)p * half + j] = (float)s;
+        }
+    x87_leave(cw);
+}
+
+/* RoPE tables: src/asm/fused_f32_kernel.inc:69-147,257-303 (plain, type 0). */
 void orc_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base)
 {
-    int half = head_dim / 2;
+    const int half = head_dim / 2;
     double freq[512];
-    for (int j = 0; j < half; ++j)
-        freq[j] = (double)powl((long double)rope_base, -(long double)j / (long double)half);
-    for (int p = 0; p < n_pos; ++p) {
-        for (int j = 0; j < half; ++j) {
-            long double a = (long double)freq[j] * (long double)p;
-            cos_table[(long long)p * half + j] = (float)cosl(a);
-            sin_table[(long long)p * half + j] = (float)sinl(a);
-        }
-    }
+    orc_rope_freqs(freq, half, rope_base);
+    rope_fill(cos_table, sin_table, n_pos, half, freq);
 }
 
 /* RoPE frequencies with Llama 3 scaling (rope type 1):
@@ -219,13 +288,14 @@ void orc_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim
 void orc_rope_freqs_llama3(double *freq, int half, float base, float factor, float low_freq_factor,
                            float high_freq_factor, int orig_max_pos)
 {
+    const unsigned short cw = x87_enter();
     const double two_pi = 6.28318530717958647692; /* rbit_two_pi */
     const long double f = (double)factor, lo = (double)low_freq_factor, hi = (double)high_freq_factor;
     const long double old = (double)orig_max_pos;
     const double low_wl = (double)(old / lo);
     const double high_wl = (double)(old / hi);
     for (int j = 0; j < half; ++j) {
-        long double inv_x = powl((long double)base, -(long double)j / (long double)half);
+        long double inv_x = ref_inv_freq(base, j, half); /* Step A, RBIT_CALC_INV_FREQ */
         double inv = (double)inv_x;
         double wavelen = (double)((long double)two_pi / inv_x);
         double ifl = (wavelen > low_wl) ? (double)((long double)inv / f) : inv;
@@ -235,17 +305,7 @@ void orc_rope_freqs_llama3(double *freq, int half, float base, float factor, flo
         int medium = wavelen >= high_wl && wavelen <= low_wl;
         freq[j] = medium ? smoothed : ifl;
     }
-}
-
-/* Tables from precomputed frequencies (the .rbit_outer / .rbit_inner fill, :257-303). */
-static void rope_fill(float *cos_table, float *sin_table, int n_pos, int half, const double *freq)
-{
-    for (int p = 0; p < n_pos; ++p)
-        for (int j = 0; j < half; ++j) {
-            long double a = (long double)freq[j] * (long double)p;
-            cos_table[(long long)p * half + j] = (float)cosl(a);
-            sin_table[(long long)p * half + j] = (float)sinl(a);
-        }
+    x87_leave(cw);
 }
 
 void orc_rope_tables_llama3(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base,

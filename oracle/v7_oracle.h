@@ -48,6 +48,8 @@ void orc_rmsnorm_rope_tokens(float *buf, int n_tokens, long long token_stride, i
                              const int32_t *positions, int rope_max_dim, float eps);
 
 /* a4: RoPE table builder (host, extended precision); tables are [n_pos, half] */
+/* Plain RoPE frequencies base^(-j/half), j < half, by the reference's x87 chain (stored as doubles). */
+void orc_rope_freqs(double *freq, int half, float base);
 void orc_rope_tables(float *cos_table, float *sin_table, int n_pos, int head_dim, float rope_base);
 void orc_rope_freqs_llama3(double *freq, int half, float base, float factor, float low_freq_factor,
                            float high_freq_factor, int orig_max_pos);

@@ -165,8 +165,7 @@ def test_v7s_rope_init_tables(shim, oracle):
     assert hip.hipMemcpy(tc.data_ptr(), c.value, n * 4, 3) == 0  # hipMemcpyDeviceToDevice
     assert hip.hipMemcpy(ts_.data_ptr(), s.value, n * 4, 3) == 0
     wc, ws = oracle.rope_tables(4096, 128, 1e6)
-    assert np.max(np.abs(tc.cpu().numpy() - wc.reshape(-1))) <= 1e-7
-    assert np.max(np.abs(ts_.cpu().numpy() - ws.reshape(-1))) <= 1e-7
+    assert bits(tc.cpu().numpy(), wc.reshape(-1)) and bits(ts_.cpu().numpy(), ws.reshape(-1))
 
 
 @pytest.mark.parametrize("size", [64, 1024, 3072, 8192])

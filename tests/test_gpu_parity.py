@@ -215,10 +215,14 @@ def test_rope_position_outside_tables_gives_nan(ops, oracle):
     assert np.isnan(got[1]).all()
 
 
-def test_rope_tables_builder(ops, oracle):
-    c, s = ops.rope_tables(4096, 128, 1e6)
-    wc, ws = oracle.rope_tables(4096, 128, 1e6)
-    assert np.max(np.abs(host(c) - wc)) <= 1e-7 and np.max(np.abs(host(s) - ws)) <= 1e-7
+@pytest.mark.parametrize("head_dim,base", [(128, 1e6), (64, 1e4), (256, 5e6)])
+def test_rope_tables_builder(ops, oracle, head_dim, base):
+    """The library's host builder runs the reference's x87 sequence (fyl2x/f2xm1/fscale frequencies, fsincos):
+    its tables equal the oracle's bit for bit."""
+    c, s = ops.rope_tables(4096, head_dim, base)
+    wc, ws = oracle.rope_tables(4096, head_dim, base)
+    assert_bits(host(c), wc, "cos")
+    assert_bits(host(s), ws, "sin")
 
 
 # --------------------------------------------------------------------------- SwiGLU (a5, a6)

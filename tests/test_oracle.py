@@ -296,6 +296,32 @@ def test_rope_tables_vs_double(oracle):
     assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
 
 
+def test_rope_freqs_x87_chain_closed_forms_and_rounding(oracle):
+    """The frequencies come from the reference's x87 chain (fyl2x, frndint, f2xm1, fscale in extended precision,
+    src/asm/fused_f32_kernel.inc:117-134) stored as doubles.  Pinned by exact closed forms (a power-of-two base
+    with j/half a dyadic fraction gives an exact power of two; j = 0 gives 1) and, for the bases models use, by
+    the correctly rounded value of base^(-j/half) from 50-digit decimal arithmetic: a 64-bit-significand chain
+    rounded once to double may differ from it by at most one ulp, and rarely does."""
+    import decimal
+
+    assert np.array_equal(oracle.rope_freqs(8, 256.0), 2.0 ** -np.arange(8))  # y = -j exactly
+    assert np.array_equal(oracle.rope_freqs(2, 4.0), [1.0, 0.5])
+    f = oracle.rope_freqs(64, 65536.0)
+    assert f[0] == 1.0 and f[16] == 2.0 ** -4 and f[32] == 2.0 ** -8 and f[48] == 2.0 ** -12
+    decimal.getcontext().prec = 50
+    total = off = 0
+    for base in (1e4, 1e5, 5e5, 1e6, 5e6):
+        for half in (32, 64, 128):
+            got = oracle.rope_freqs(half, base)
+            for j in range(half):
+                exact = float(decimal.Decimal(base) ** (decimal.Decimal(-j) / decimal.Decimal(half)))
+                total += 1
+                if got[j] != exact:
+                    off += 1
+                    assert abs(got[j] - exact) <= np.spacing(exact), (base, half, j)
+    assert off <= total // 100, (off, total)
+
+
 LLAMA31 = dict(base=500000.0, factor=8.0, low=1.0, high=4.0, orig=8192)  # Llama 3.1 8B config.json
 
 

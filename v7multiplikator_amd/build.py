@@ -42,15 +42,38 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
+# Host-only C++ (x87 RoPE table builder): compiled by g++ and linked into the library.
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-Wall"]
+
+
+def host_sources():
+    return sorted(glob.glob(os.path.join(CSRC, "*.cpp")))
+
+
 def build_library(verbose: bool = False) -> str:
-    """Compiles every csrc/*.hip into libv7g.so; returns its path."""
+    """Compiles every csrc/*.hip (hipcc, gfx950) and the host-only table builder (g++) into libv7g.so;
+    returns its path."""
     tmp = LIB + ".tmp"
+    objs = []
+    for src in host_sources():
+        if os.path.basename(src) == "v7g_loadtest.cpp":
+            continue
+        obj = os.path.join(PKG, os.path.basename(src) + ".o")
+        cmd = ["g++", *HOST_FLAGS, "-c", "-o", obj, src]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"g++ failed ({res.returncode}):\n{res.stdout}{res.stderr}")
+        objs.append(obj)
     exports = os.path.join(CSRC, "v7g_exports.map")
     cmd = [hipcc(), *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), f"-Wl,--version-script={exports}", "-o", tmp,
-           *sources()]
+           *sources(), "-x", "none", *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
+    for obj in objs:
+        os.remove(obj)
     out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in l)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "v7g_alias.h"
+#include "v7g_rope_tables.h"
 #include "v7g_internal.h"
 #include "../../include/v7g_lib.h"
 
@@ -190,63 +191,10 @@ int check_rope_alias(const v7g::RopeSide *sides, int n_sides, int n_tokens, int 
   return V7G_OK;
 }
 
-// Host RoPE table builder: src/asm/fused_f32_kernel.inc:69-303.  The
-// frequencies are computed in extended precision and kept as doubles, as the
-// reference's x87 code stores them; angle = freq_j * pos in extended
-// precision; cos/sin rounded to float.
-
-// Plain tables (rope type 0, :120-147): freq_j = base^(-j/half).
-std::vector<double> plain_freqs(int half, float base) {
-  std::vector<double> freq(half);
-  for (int j = 0; j < half; ++j)
-    freq[j] = (double)std::pow((long double)base, -(long double)j / (long double)half);
-  return freq;
-}
-
-// Llama 3 frequency scaling (rope type 1, :149-256), the values rounded to
-// double where the reference stores them: wavelen_j = 2 pi / inv_j; below the
-// high-frequency wavelength inv_j is kept, above the low-frequency wavelength
-// it is divided by factor, and in between it is interpolated with
-// smooth = (orig/wavelen - low) / (high - low).
-std::vector<double> llama3_freqs(int half, float base, float factor, float low_freq_factor, float high_freq_factor,
-                                 int orig_max_pos) {
-  typedef long double X;
-  const double two_pi = 6.28318530717958647692;
-  const double f = factor, lo = low_freq_factor, hi = high_freq_factor, old = orig_max_pos;
-  const double low_wl = (double)((X)old / (X)lo);
-  const double high_wl = (double)((X)old / (X)hi);
-  std::vector<double> freq(half);
-  for (int j = 0; j < half; ++j) {
-    const X inv_x = std::pow((X)base, -(X)j / (X)half);
-    const double inv = (double)inv_x;
-    const double wavelen = (double)((X)two_pi / inv_x);
-    const double ifl = wavelen > low_wl ? (double)((X)inv / (X)f) : inv;
-    const double smooth = (double)(((X)old / (X)wavelen - (X)lo) / ((X)hi - (X)lo));
-    const double smoothed = (double)((1.0L - (X)smooth) * ((X)ifl / (X)f) + (X)smooth * (X)ifl);
-    const bool medium = wavelen >= high_wl && wavelen <= low_wl;
-    freq[j] = medium ? smoothed : ifl;
-  }
-  return freq;
-}
-
-void fill_tables(std::vector<float> &c, std::vector<float> &s, int n_pos, const std::vector<double> &freq) {
-  const int half = (int)freq.size();
-  c.resize((size_t)n_pos * half);
-  s.resize((size_t)n_pos * half);
-  unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-  std::vector<std::thread> th;
-  for (unsigned w = 0; w < nt; ++w) {
-    th.emplace_back([&, w]() {
-      for (int p = (int)w; p < n_pos; p += (int)nt)
-        for (int j = 0; j < half; ++j) {
-          long double a = (long double)freq[j] * (long double)p;
-          c[(size_t)p * half + j] = (float)std::cos(a);
-          s[(size_t)p * half + j] = (float)std::sin(a);
-        }
-    });
-  }
-  for (auto &t : th) t.join();
-}
+// The RoPE table builders (x87, host only) live in v7g_rope_tables.cpp.
+using v7g::fill_tables;
+using v7g::llama3_freqs;
+using v7g::plain_freqs;
 
 int check_table_shape(int n_pos, int head_dim) {
   return (n_pos <= 0 || n_pos > kRopeMaxPositions || head_dim < 2 || head_dim % 2 != 0 || head_dim > 1024)
