@@ -29,11 +29,63 @@
 
 namespace v7g {
 
+// The chain lane lam runs YMM accumulator q = v >> 3, lane j = v & 7 with
+// v = chain_of_lane(lam), chosen so that lam = 8*q0 + 4*q1 + 2*j2 + j0 + 16*j1
+// (q0, q1, j0..j2 the bits of q and j): the reduction's pairs are then lanes
+// lam, lam+8 (A+B, C+D), lam, lam+4 ((A+B)+(C+D)), lam, lam+2 (v_i + v_{i+4}),
+// lam, lam+1 (w0+w1, w2+w3) and lanes 0, 16 (the final sum).
+__device__ __forceinline__ int chain_of_lane(int lam) {
+  const int q = ((lam >> 3) & 1) | (((lam >> 2) & 1) << 1);
+  const int j = (lam & 1) | (((lam >> 4) & 1) << 1) | (((lam >> 1) & 1) << 2);
+  return 8 * q + j;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum of squares of a row of dim floats (dim % 32 == 0) staged at the padded
+// layout, in the reference's order; called by a whole wave, returns the same
+// value in every lane.
+__device__ __forceinline__ float padded_row_sumsq(const float *row, int dim) {
+  const int lane = __lane_id();
+  float acc = 0.0f;
+  if (lane < 32) {
+    const int v = chain_of_lane(lane);
+    // element 32g + v sits at float 40g + v + 4*(v >> 4)
+    const float *p = row + v + 4 * (v >> 4);
+    const int steps = dim >> 5;
+#pragma unroll 16
+    for (int g = 0; g < steps; ++g) {
+      const float e = p[40 * g];
+      acc = __builtin_fmaf(e, e, acc);
+    }
+  }
+  acc = acc + dpp_f<0x108>(acc);  // row_shl:8   A+B, C+D
+  acc = acc + dpp_f<0x104>(acc);  // row_shl:4   (A+B)+(C+D)
+  acc = acc + dpp_f<0x102>(acc);  // row_shl:2   HADD_YMM: v_i + v_{i+4}
+  acc = acc + dpp_f<0x101>(acc);  // row_shl:1   w0+w1, w2+w3
+  const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
+  const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 16));
+  return lo + hi;
+}
+
+// A workgroup barrier for LDS only: unlike __syncthreads() it does not wait
+// for the wave's global loads and stores (s_waitcnt lgkmcnt(0), not vmcnt).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ int padded(int m) { return 4 * (m + (m >> 2)); }
+
 // One row.  ADD: the input is residual + add (residual updated in place),
 // else x.  QGS == 0: o = (s*x)*w; QGS = 32 or 64: the normalised row is
 // quantized in groups of QGS (codes q, scales q_s) and o is not written.
 // o may alias residual (the row then ends as o, as in the reference).
-template <int TPR, int KMAX, bool ADD, int QGS>
+// PAD (dim % 32 == 0, dim <= 12288): the row is staged at the padded layout and
+// the chains' reduction runs as DPP row shifts (padded_row_sumsq); otherwise
+// at the natural layout with the lane-exchange reduction, which also covers
+// the leftover 8-float blocks of dim % 32 != 0.
+template <int TPR, int KMAX, bool ADD, int QGS, bool PAD>
 __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *xin, const float *add,
                                         const float *weight, int dim, float eps) {
   extern __shared__ float row[];
@@ -59,12 +111,18 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
         x[k] = make_float4(x[k].x + b[k].x, x[k].y + b[k].y, x[k].z + b[k].z, x[k].w + b[k].w);
         st_stream4(xr + i, x[k]);
       }
-      *reinterpret_cast<float4 *>(row + i) = x[k];
+      *reinterpret_cast<float4 *>(row + (PAD ? padded(tid + k * TPR) : i)) = x[k];
     }
   }
   __syncthreads();
 
-  if (tid < 64) {
+  if constexpr (PAD) {
+    // floats 16..19 of the padded layout are padding: the scale goes there
+    if (tid < 64) {
+      const float s0 = rms_scale(padded_row_sumsq(row, dim), (float)dim, eps);
+      if (tid == 0) row[16] = s0;
+    }
+  } else if (tid < 64) {
     // The 32 FMA chains: lane v = 8q + j is YMM accumulator q (A..D), lane j.
     float acc = 0.0f;
     if (tid < 32) {
@@ -93,7 +151,7 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
     if (tid == 0) row[0] = rms_scale(acc, (float)dim, eps);
   }
   __syncthreads();
-  const float s = row[0];
+  const float s = row[PAD ? 16 : 0];
 
   // Pass 2: n = (s * x) * w, then either stored or quantized.
 #pragma unroll
@@ -151,54 +209,6 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
 // rms_row, so the same bits; about 10% less time at [8192, 4096] than
 // rms_row, whose 4-element-per-lane quantizer and lane-exchange reduction
 // made the kernel issue-bound.
-
-// The chain lane lam runs YMM accumulator q = v >> 3, lane j = v & 7 with
-// v = chain_of_lane(lam), chosen so that lam = 8*q0 + 4*q1 + 2*j2 + j0 + 16*j1
-// (q0, q1, j0..j2 the bits of q and j): the reduction's pairs are then lanes
-// lam, lam+8 (A+B, C+D), lam, lam+4 ((A+B)+(C+D)), lam, lam+2 (v_i + v_{i+4}),
-// lam, lam+1 (w0+w1, w2+w3) and lanes 0, 16 (the final sum).
-__device__ __forceinline__ int chain_of_lane(int lam) {
-  const int q = ((lam >> 3) & 1) | (((lam >> 2) & 1) << 1);
-  const int j = (lam & 1) | (((lam >> 4) & 1) << 1) | (((lam >> 1) & 1) << 2);
-  return 8 * q + j;
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum of squares of a row of dim floats (dim % 32 == 0) staged at the padded
-// layout, in the reference's order; called by a whole wave, returns the same
-// value in every lane.
-__device__ __forceinline__ float padded_row_sumsq(const float *row, int dim) {
-  const int lane = __lane_id();
-  float acc = 0.0f;
-  if (lane < 32) {
-    const int v = chain_of_lane(lane);
-    // element 32g + v sits at float 40g + v + 4*(v >> 4)
-    const float *p = row + v + 4 * (v >> 4);
-    const int steps = dim >> 5;
-#pragma unroll 16
-    for (int g = 0; g < steps; ++g) {
-      const float e = p[40 * g];
-      acc = __builtin_fmaf(e, e, acc);
-    }
-  }
-  acc = acc + dpp_f<0x108>(acc);  // row_shl:8   A+B, C+D
-  acc = acc + dpp_f<0x104>(acc);  // row_shl:4   (A+B)+(C+D)
-  acc = acc + dpp_f<0x102>(acc);  // row_shl:2   HADD_YMM: v_i + v_{i+4}
-  acc = acc + dpp_f<0x101>(acc);  // row_shl:1   w0+w1, w2+w3
-  const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
-  const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 16));
-  return lo + hi;
-}
-
-// A workgroup barrier for LDS only: unlike __syncthreads() it does not wait
-// for the wave's global loads and stores (s_waitcnt lgkmcnt(0), not vmcnt).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-__device__ __forceinline__ int padded(int m) { return 4 * (m + (m >> 2)); }
 
 // TPB > 0: the block size, known at compile time (the common widths); 0: blockDim.x.
 template <int TPB, int QGS, bool ADD>
@@ -282,28 +292,28 @@ __global__ __launch_bounds__(TPB ? TPB : 1024) void norm_q8_row16_kernel(int8_t 
   st_stream_f32(q_s + r * (size_t)(dim / QGS) + t / (QGS / 16), scale);
 }
 
-template <int TPR, int KMAX>
+template <int TPR, int KMAX, bool PAD>
 __global__ __launch_bounds__(TPR) void fused_add_rmsnorm_kernel(float *o, float *residual, const float *add,
                                                                 const float *weight, int dim, float eps) {
-  rms_row<TPR, KMAX, true, 0>(o, nullptr, nullptr, residual, add, weight, dim, eps);
+  rms_row<TPR, KMAX, true, 0, PAD>(o, nullptr, nullptr, residual, add, weight, dim, eps);
 }
 
-template <int TPR, int KMAX>
+template <int TPR, int KMAX, bool PAD>
 __global__ __launch_bounds__(TPR) void rmsnorm_kernel(float *o, float *x, const float *weight, int dim, float eps) {
-  rms_row<TPR, KMAX, false, 0>(o, nullptr, nullptr, x, nullptr, weight, dim, eps);
+  rms_row<TPR, KMAX, false, 0, PAD>(o, nullptr, nullptr, x, nullptr, weight, dim, eps);
 }
 
-template <int TPR, int KMAX, int QGS>
+template <int TPR, int KMAX, int QGS, bool PAD>
 __global__ __launch_bounds__(TPR) void rmsnorm_quantize_kernel(int8_t *q, float *q_s, float *x, const float *weight,
                                                                int dim, float eps) {
-  rms_row<TPR, KMAX, false, QGS>(nullptr, q, q_s, x, nullptr, weight, dim, eps);
+  rms_row<TPR, KMAX, false, QGS, PAD>(nullptr, q, q_s, x, nullptr, weight, dim, eps);
 }
 
-template <int TPR, int KMAX, int QGS>
+template <int TPR, int KMAX, int QGS, bool PAD>
 __global__ __launch_bounds__(TPR) void add_rmsnorm_quantize_kernel(int8_t *q, float *q_s, float *residual,
                                                                    const float *add, const float *weight, int dim,
                                                                    float eps) {
-  rms_row<TPR, KMAX, true, QGS>(nullptr, q, q_s, residual, add, weight, dim, eps);
+  rms_row<TPR, KMAX, true, QGS, PAD>(nullptr, q, q_s, residual, add, weight, dim, eps);
 }
 
 // Chooses threads per row and float4 chunks per thread for dim <= 16384
@@ -311,7 +321,9 @@ __global__ __launch_bounds__(TPR) void add_rmsnorm_quantize_kernel(int8_t *q, fl
 struct RowLaunch {
   int rows, dim;
   hipStream_t stream;
-  size_t lds() const { return (size_t)dim * sizeof(float); }
+  // the padded layout and DPP reduction: whole 32-float blocks, at most 64 KiB of LDS (5 bytes per element)
+  bool pad() const { return dim % 32 == 0 && dim <= 12288; }
+  size_t lds() const { return (size_t)(pad() ? dim + dim / 4 : dim) * sizeof(float); }
 };
 
 template <template <int, int> class Op, typename... A>
@@ -333,16 +345,24 @@ static void dispatch_rows(const RowLaunch &L, A... args) {
 template <int TPR, int KMAX>
 struct AddNormOp {
   static void launch(const RowLaunch &L, float *o, float *residual, const float *add, const float *weight, float eps) {
-    enqueue((fused_add_rmsnorm_kernel<TPR, KMAX>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, o,
-                       residual, add, weight, L.dim, eps);
+    auto go = [&](auto kernel) {
+      enqueue(kernel, dim3(L.rows), dim3(TPR), L.lds(), L.stream, o, residual, add, weight, L.dim, eps);
+    };
+    if (L.pad())
+      go(fused_add_rmsnorm_kernel<TPR, KMAX, true>);
+    else
+      go(fused_add_rmsnorm_kernel<TPR, KMAX, false>);
   }
 };
 
 template <int TPR, int KMAX>
 struct NormOp {
   static void launch(const RowLaunch &L, float *o, float *x, const float *weight, float eps) {
-    enqueue((rmsnorm_kernel<TPR, KMAX>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, o, x, weight, L.dim,
-                       eps);
+    auto go = [&](auto kernel) { enqueue(kernel, dim3(L.rows), dim3(TPR), L.lds(), L.stream, o, x, weight, L.dim, eps); };
+    if (L.pad())
+      go(rmsnorm_kernel<TPR, KMAX, true>);
+    else
+      go(rmsnorm_kernel<TPR, KMAX, false>);
   }
 };
 
@@ -350,20 +370,25 @@ template <int TPR, int KMAX>
 struct NormQ8Op {
   static void launch(const RowLaunch &L, int8_t *q, float *q_s, float *x, const float *add, const float *weight,
                      float eps, int gs) {
+    auto go_add = [&](auto kernel) {
+      enqueue(kernel, dim3(L.rows), dim3(TPR), L.lds(), L.stream, q, q_s, x, add, weight, L.dim, eps);
+    };
+    auto go = [&](auto kernel) {
+      enqueue(kernel, dim3(L.rows), dim3(TPR), L.lds(), L.stream, q, q_s, x, weight, L.dim, eps);
+    };
+    const bool pad = L.pad();
     if (add) {
       if (gs == 32)
-        enqueue((add_rmsnorm_quantize_kernel<TPR, KMAX, 32>), dim3(L.rows), dim3(TPR), L.lds(), L.stream,
-                           q, q_s, x, add, weight, L.dim, eps);
+        pad ? go_add(add_rmsnorm_quantize_kernel<TPR, KMAX, 32, true>)
+            : go_add(add_rmsnorm_quantize_kernel<TPR, KMAX, 32, false>);
       else
-        enqueue((add_rmsnorm_quantize_kernel<TPR, KMAX, 64>), dim3(L.rows), dim3(TPR), L.lds(), L.stream,
-                           q, q_s, x, add, weight, L.dim, eps);
+        pad ? go_add(add_rmsnorm_quantize_kernel<TPR, KMAX, 64, true>)
+            : go_add(add_rmsnorm_quantize_kernel<TPR, KMAX, 64, false>);
     } else {
       if (gs == 32)
-        enqueue((rmsnorm_quantize_kernel<TPR, KMAX, 32>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, q,
-                           q_s, x, weight, L.dim, eps);
+        pad ? go(rmsnorm_quantize_kernel<TPR, KMAX, 32, true>) : go(rmsnorm_quantize_kernel<TPR, KMAX, 32, false>);
       else
-        enqueue((rmsnorm_quantize_kernel<TPR, KMAX, 64>), dim3(L.rows), dim3(TPR), L.lds(), L.stream, q,
-                           q_s, x, weight, L.dim, eps);
+        pad ? go(rmsnorm_quantize_kernel<TPR, KMAX, 64, true>) : go(rmsnorm_quantize_kernel<TPR, KMAX, 64, false>);
     }
   }
 };
