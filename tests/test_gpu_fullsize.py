@@ -113,3 +113,29 @@ def test_c5d_swiglu_q8_full(ops, oracle):
     # half a step, plus the f32 SwiGLU's own error (within 1e-5 relative of double)
     bound = 0.5 * np.repeat(gs[:16], 32, axis=1).astype(np.float64) + 2e-5 * np.abs(ref)
     assert np.all(np.abs(deq.reshape(16, -1) - ref) <= bound)
+
+
+def test_next_rows_full(ops, oracle):
+    """The widened rows at the same shape: RMSNorm -> Q8 and the fused add -> RMSNorm -> Q8 at [8192, 4096]
+    GS 64 (the Q8 path's per-layer input), and the K/V rows of the fused QKV rows packed to two binary16
+    caches in one launch; bit for bit.  Size-independent property: every code lies in [-127, 127] and the
+    largest |code| of each group is 127 (the group max maps to 127 exactly)."""
+    x = C.normal(531, (T, DIM))
+    a = C.normal(532, (T, DIM))
+    w = C.norm_weight(533, DIM)
+    wq, ws = oracle.rmsnorm_quantize(x, w, 1e-6, 64)
+    q, s = ops.rmsnorm_quantize(dev(x), dev(w), eps=1e-6, gs=64)
+    gq = host(q)
+    assert same(gq, wq) and same(host(s), ws)
+    assert np.all(np.abs(gq.reshape(-1, 64).astype(np.int32)).max(axis=1) == 127)
+    xt = dev(x)
+    q, s = ops.add_rmsnorm_quantize(xt, dev(a), dev(w), eps=1e-6, gs=64)
+    summed = oracle.add_inplace(x, a)
+    wq, ws = oracle.rmsnorm_quantize(summed, w, 1e-6, 64)
+    assert same(host(xt), summed) and same(host(q), wq) and same(host(s), ws)
+    qkv = C.normal(534, (T, (NQ + 2 * NKV) * HD))
+    d = dev(qkv)
+    k0, v0 = NQ * HD, (NQ + NKV) * HD
+    hk, hv = ops.kv_pack_f16_kv(d[:, k0:v0], d[:, v0:])
+    assert same(host(hk).view(np.uint16), oracle.kv_pack_f16(qkv[:, k0:v0]))
+    assert same(host(hv).view(np.uint16), oracle.kv_pack_f16(qkv[:, v0:]))

@@ -155,3 +155,11 @@ def test_sweep_embedding_and_kv_pack(ops, oracle):
         x = C.normal(n + dim, (n, dim), 8.0)
         h = host(ops.kv_pack_f16(dev(x))).view(np.uint16)
         assert same(h, oracle.kv_pack_f16(x)), ("kv_pack", n, dim)
+        # K and V of fused rows [Q | K | V] (Q of a drawn width) in one launch
+        kv = dim // 4 * 4 - 4 if dim > 64 else dim
+        q_w = 4 * (dim % 13)
+        qkv = C.normal(n + dim + 2, (n, q_w + 2 * kv), 8.0)
+        d = dev(qkv)
+        hk, hv = ops.kv_pack_f16_kv(d[:, q_w:q_w + kv], d[:, q_w + kv:])
+        assert same(host(hk).view(np.uint16), oracle.kv_pack_f16(qkv[:, q_w:q_w + kv])), ("kv_pack K", n, kv, q_w)
+        assert same(host(hv).view(np.uint16), oracle.kv_pack_f16(qkv[:, q_w + kv:])), ("kv_pack V", n, kv, q_w)
