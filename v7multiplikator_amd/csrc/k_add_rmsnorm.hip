@@ -47,7 +47,8 @@ __device__ __forceinline__ float dpp_f(float v) {
 
 // Sum of squares of a row of dim floats (dim % 32 == 0) staged at the padded
 // layout, in the reference's order; called by a whole wave, returns the same
-// value in every lane.
+// value in every lane.  U: chain elements per register set (2U VGPRs).
+template <int U>
 __device__ __forceinline__ float padded_row_sumsq(const float *row, int dim) {
   const int lane = __lane_id();
   float acc = 0.0f;
@@ -56,10 +57,42 @@ __device__ __forceinline__ float padded_row_sumsq(const float *row, int dim) {
     // element 32g + v sits at float 40g + v + 4*(v >> 4)
     const float *p = row + v + 4 * (v >> 4);
     const int steps = dim >> 5;
+    if (steps % (2 * U) == 0) {
+      // Two register sets of U chain elements: the LDS reads of one set are
+      // in flight while the FMAs consume the other, so the chain waits on
+      // LDS once instead of once per U steps.  Same FMAs, same order.  The
+      // empty asm statements pass the accumulator through a point after each
+      // set of reads, so the compiler neither sinks a read down to its use
+      // nor hoists the FMAs above the reads of the other set.
+      float a[U], b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) a[u] = p[40 * u];
+      int g0 = 0;
+      for (; g0 + 2 * U < steps; g0 += 2 * U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) b[u] = p[40 * (g0 + U + u)];
+        asm volatile("" : "+v"(acc)::"memory");
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = __builtin_fmaf(a[u], a[u], acc);
+#pragma unroll
+        for (int u = 0; u < U; ++u) a[u] = p[40 * (g0 + 2 * U + u)];
+        asm volatile("" : "+v"(acc)::"memory");
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = __builtin_fmaf(b[u], b[u], acc);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = p[40 * (g0 + U + u)];
+      asm volatile("" : "+v"(acc)::"memory");
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc = __builtin_fmaf(a[u], a[u], acc);
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc = __builtin_fmaf(b[u], b[u], acc);
+    } else {
 #pragma unroll 16
-    for (int g = 0; g < steps; ++g) {
-      const float e = p[40 * g];
-      acc = __builtin_fmaf(e, e, acc);
+      for (int g = 0; g < steps; ++g) {
+        const float e = p[40 * g];
+        acc = __builtin_fmaf(e, e, acc);
+      }
     }
   }
   acc = acc + dpp_f<0x108>(acc);  // row_shl:8   A+B, C+D
@@ -88,7 +121,7 @@ __device__ __forceinline__ int padded(int m) { return 4 * (m + (m >> 2)); }
 template <int TPR, int KMAX, bool ADD, int QGS, bool PAD>
 __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *xin, const float *add,
                                         const float *weight, int dim, float eps) {
-  extern __shared__ float row[];
+  extern __shared__ __attribute__((aligned(16))) float row[];
   const int tid = threadIdx.x;
   const size_t r = blockIdx.x;
   float *xr = xin + r * (size_t)dim;
@@ -119,7 +152,7 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
   if constexpr (PAD) {
     // floats 16..19 of the padded layout are padding: the scale goes there
     if (tid < 64) {
-      const float s0 = rms_scale(padded_row_sumsq(row, dim), (float)dim, eps);
+      const float s0 = rms_scale(padded_row_sumsq<8>(row, dim), (float)dim, eps);
       if (tid == 0) row[16] = s0;
     }
   } else if (tid < 64) {
@@ -208,14 +241,18 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
 // residual back with the loads' layout.  Same operations and order as
 // rms_row, so the same bits; about 10% less time at [8192, 4096] than
 // rms_row, whose 4-element-per-lane quantizer and lane-exchange reduction
-// made the kernel issue-bound.
+// made the kernel issue-bound.  The LDS array is declared 16-byte aligned:
+// with the element type's 4-byte alignment the compiler splits every float4
+// access into two 8-byte ones.  The chains read their elements one register
+// set ahead (16 elements; 8 in the fused-add form, which keeps the weights
+// live across the chain and would otherwise exceed 64 VGPRs).
 
 // TPB > 0: the block size, known at compile time (the common widths); 0: blockDim.x.
 template <int TPB, int QGS, bool ADD>
 __global__ __launch_bounds__(TPB ? TPB : 1024) void norm_q8_row16_kernel(int8_t *q, float *q_s, float *x,
                                                                          const float *add, const float *weight,
                                                                          int dim, float eps) {
-  extern __shared__ float row[];  // dim + dim/4 floats; floats 16..19 (padding) hold the scale
+  extern __shared__ __attribute__((aligned(16))) float row[];  // dim + dim/4 floats; floats 16..19 (padding) hold the scale
   const int t = threadIdx.x;
   const int T = TPB ? TPB : (int)blockDim.x;  // dim / 16
   if constexpr (TPB > 0) dim = 16 * TPB;
@@ -245,7 +282,7 @@ __global__ __launch_bounds__(TPB ? TPB : 1024) void norm_q8_row16_kernel(int8_t 
   for (int k = 0; k < 4; ++k) *reinterpret_cast<float4 *>(row + padded(t + k * T)) = v[k];
   lds_barrier();
   if (t < 64) {
-    const float s0 = rms_scale(padded_row_sumsq(row, dim), (float)dim, eps);
+    const float s0 = rms_scale(padded_row_sumsq<ADD ? 8 : 16>(row, dim), (float)dim, eps);
     if (t == 0) row[16] = s0;
   }
   if constexpr (!ADD) {
