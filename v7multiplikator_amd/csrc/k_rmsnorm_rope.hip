@@ -207,7 +207,7 @@ template <int K>
 __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
   constexpr int HD = 32 * K;
   constexpr int HALF = HD / 2;
-  __shared__ float lds[32 * HD];
+  __shared__ __attribute__((aligned(16))) float lds[32 * HD];  // 16-byte LDS stores of the float4 chunks
   const int m = threadIdx.x & 7;
   const unsigned unit = (blockIdx.x * 256u + threadIdx.x) >> 3;
   const HeadRef hr = head_ref(a, unit, m);
