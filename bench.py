@@ -20,12 +20,18 @@ timed region; `roofline` reports the dominant kernel (SwiGLU -> Q8) against the
 times the AVX2 restatement of the reference kernels on the host cores, driven
 per token row as the reference engine drives them, on a bounded sample of the
 same workload; that leg also checks the GPU outputs of the sample bit for bit.
+With V7_REF_SO naming a libv7_threading.so built by the reference's own
+Makefile (nasm), `cpu_baseline.reference` adds that library's two exported
+chain kernels (add+RMSNorm, Q/K RMSNorm+RoPE) on the same sample, beside the
+restatement's same two kernels and checked against them bit for bit
+(V7_REF_EPS: the eps its g_rms_eps global holds, 0 without its database init).
 
     python bench.py [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -127,11 +133,19 @@ class Chain:
         ]
 
 
+class ChainArgs(ctypes.Structure):
+    """orc_chain_args (oracle/v7_oracle.h): shapes, eps and the host buffers of one chain sample."""
+    _fields_ = [(n, ctypes.c_int) for n in
+                ("n_tokens", "dim", "n_q_heads", "n_kv_heads", "head_dim", "rope_max_dim", "hidden", "gs")] + [
+        ("eps", ctypes.c_float)] + [(n, ctypes.c_void_p) for n in
+                                    ("ids", "positions", "table_q", "table_s", "emb_out", "residual", "add",
+                                     "w_norm", "normed", "q", "k", "q_w", "k_w", "cos_table", "sin_table",
+                                     "gate", "up", "act", "codes", "scales")]
+
+
 def cpu_baseline(torch, ops, chain, args):
     """Times the AVX2 restatement of the reference kernels (oracle/, "port") on a sample of the workload and
     checks the GPU chain bit for bit on the same sample."""
-    import ctypes
-
     import numpy as np
 
     from oracle import oracle as O
@@ -152,28 +166,24 @@ def cpu_baseline(torch, ops, chain, args):
     gate = hostc(chain.gate[:S])
     up = hostc(chain.up[:S])
 
-    class Args(ctypes.Structure):
-        _fields_ = [(n, ctypes.c_int) for n in
-                    ("n_tokens", "dim", "n_q_heads", "n_kv_heads", "head_dim", "rope_max_dim", "hidden", "gs")] + [
-            ("eps", ctypes.c_float)] + [(n, ctypes.c_void_p) for n in
-                                        ("ids", "positions", "table_q", "table_s", "emb_out", "residual", "add",
-                                         "w_norm", "normed", "q", "k", "q_w", "k_w", "cos_table", "sin_table",
-                                         "gate", "up", "act", "codes", "scales")]
+    Args = ChainArgs
+
+    def make_args(n, residual, q, k, eps=EPS):
+        out = dict(emb=np.empty((S, DIM), np.float32), normed=np.empty((S, DIM), np.float32),
+                   act=np.empty((S, HIDDEN), np.float32), codes=np.empty((S, HIDDEN), np.int8),
+                   scales=np.empty((S, HIDDEN // GS), np.float32))
+        p = lambda a: a.ctypes.data  # noqa: E731
+        a = Args(n, DIM, NQ, NKV, HD, HD // 2, HIDDEN, GS, eps, p(ids), p(positions), p(table_q), p(table_s),
+                 p(out["emb"]), p(residual), p(add), p(w_norm), p(out["normed"]), p(q), p(k), p(q_w), p(k_w), p(cos_t),
+                 p(sin_t), p(gate), p(up), p(out["act"]), p(out["codes"]), p(out["scales"]))
+        return a, out
 
     def run(reps, n_threads, residual, q, k, n=S):
-        emb = np.empty((S, DIM), np.float32)
-        normed = np.empty((S, DIM), np.float32)
-        act = np.empty((S, HIDDEN), np.float32)
-        codes = np.empty((S, HIDDEN), np.int8)
-        scales = np.empty((S, HIDDEN // GS), np.float32)
-        p = lambda a: a.ctypes.data  # noqa: E731
-        a = Args(n, DIM, NQ, NKV, HD, HD // 2, HIDDEN, GS, EPS, p(ids), p(positions), p(table_q), p(table_s), p(emb),
-                 p(residual), p(add), p(w_norm), p(normed), p(q), p(k), p(q_w), p(k_w), p(cos_t), p(sin_t), p(gate),
-                 p(up), p(act), p(codes), p(scales))
+        a, out = make_args(n, residual, q, k)
         L.orc_avx2_chain_bench.restype = ctypes.c_double
         L.orc_avx2_chain_bench.argtypes = [ctypes.POINTER(Args), ctypes.c_int, ctypes.c_int]
         secs = L.orc_avx2_chain_bench(ctypes.byref(a), n_threads, reps)
-        return secs, emb, normed, codes, scales
+        return secs, out["emb"], out["normed"], out["codes"], out["scales"]
 
     try:
         cores = len(os.sched_getaffinity(0))
@@ -226,6 +236,11 @@ def cpu_baseline(torch, ops, chain, args):
     # sample (the same rows, still beyond the host caches) for a quarter of the time.
     n1 = max(1, S // 4)
     gbs1, reps1, secs1 = timed(1, n1, args.cpu_seconds / 4)
+    ref_so = os.environ.get("V7_REF_SO")
+    reference = None
+    if ref_so:
+        reference = reference_leg(L, Args, make_args, residual0, q_h, k_h, S, cores, ref_so,
+                                  float(os.environ.get("V7_REF_EPS", "0")), args.cpu_seconds)
     return {
         "value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
         "sample": f"{S} of the {T} tokens of the same chain (same shapes; working set larger than the host "
@@ -236,6 +251,57 @@ def cpu_baseline(torch, ops, chain, args):
                           "sample": f"{n1} tokens, {reps1} repetitions in {secs1:.1f} s"},
         "cpu_model": cpu_model(),
         "gpu_sample_bit_exact": match,
+        **({"reference": reference} if reference is not None else {}),
+    }
+
+
+def reference_leg(L, Args, make_args, residual0, q0, k0, S, cores, path, eps, seconds):
+    """The reference library itself (a libv7_threading.so built by its own Makefile, named by V7_REF_SO) on
+    the two kernels of the chain it exports, v7s_fused_add_rmsnorm and v7s_rmsnorm_rope_heads
+    (src/v7_threading.def, src/v7_lib.h:272-273), timed per token row over the same sample and threads as
+    the restatement, whose same two kernels are timed beside it.  The library's norm kernels read eps from
+    its g_rms_eps global, 0 unless its database init ran: V7_REF_EPS names the value it holds, and the
+    restatement computes with it, so the two outputs are compared bit for bit."""
+    import numpy as np
+
+    L.orc_ref_open.restype = ctypes.c_int
+    L.orc_ref_open.argtypes = [ctypes.c_char_p]
+    L.orc_ref_error.restype = ctypes.c_char_p
+    L.orc_k23_bench.restype = ctypes.c_double
+    L.orc_k23_bench.argtypes = [ctypes.POINTER(Args), ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    rc = L.orc_ref_open(path.encode())
+    if rc != 0:
+        return {"so": path, "error": L.orc_ref_error().decode(errors="replace")}
+    try:
+        outs = []
+        for use_ref in (1, 0):
+            r, q, k = residual0.copy(), q0.copy(), k0.copy()
+            a, out = make_args(S, r, q, k, eps)
+            L.orc_k23_bench(ctypes.byref(a), cores, 1, use_ref)
+            outs.append((r, q, k, out["normed"]))
+        same = all(np.array_equal(x.view(np.uint32), y.view(np.uint32)) for x, y in zip(*outs))
+        k23_bytes = (BYTES["fused_add_rmsnorm"] + BYTES["qk_rmsnorm_rope"]) * S / T
+        res = {}
+        for name, use_ref in (("reference", 1), ("port", 0)):
+            r, q, k = residual0.copy(), q0.copy(), k0.copy()
+            a, _ = make_args(S, r, q, k, eps)
+            L.orc_k23_bench(ctypes.byref(a), cores, 1, use_ref)
+            secs, reps, chunk = 0.0, 0, 1
+            while secs < seconds / 2:
+                t = L.orc_k23_bench(ctypes.byref(a), cores, chunk, use_ref)
+                secs += t
+                reps += chunk
+                chunk = max(1, min(chunk * 4, int((seconds / 2 - secs) / max(t / chunk, 1e-6)) + 1))
+            res[name] = (k23_bytes * reps / secs / 1e9, reps, secs)
+    finally:
+        L.orc_ref_close()
+    return {
+        "so": path, "kernels": ["v7s_fused_add_rmsnorm", "v7s_rmsnorm_rope_heads"], "eps": eps,
+        "value": round(res["reference"][0], 3), "unit": "GB/s", "cores": cores,
+        "port_same_kernels": round(res["port"][0], 3),
+        "bit_exact_vs_port": bool(same),
+        "sample": f"add+RMSNorm and Q/K RMSNorm+RoPE of {S} tokens per row, {res['reference'][1]} repetitions "
+                  f"in {res['reference'][2]:.1f} s",
     }
 
 
@@ -243,8 +309,6 @@ class HipEvents:
     """Timing events of the HIP runtime, created with hipEventDisableSystemFence (0x20000000)."""
 
     def __init__(self):
-        import ctypes
-
         self.ct = ctypes
         self.hip = ctypes.CDLL("libamdhip64.so")
         self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]

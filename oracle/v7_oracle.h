@@ -134,6 +134,13 @@ typedef struct orc_chain_args {
  * n_threads host threads.  Returns wall seconds. */
 double orc_avx2_chain_bench(const orc_chain_args *a, int n_threads, int reps);
 
+/* The reference binary as a baseline (v7_ref_leg.c): loads a libv7_threading.so by path and times its
+ * two exported chain kernels, v7s_fused_add_rmsnorm and v7s_rmsnorm_rope_heads, per token row. */
+int orc_ref_open(const char *path);
+void orc_ref_close(void);
+const char *orc_ref_error(void);
+double orc_k23_bench(const orc_chain_args *a, int n_threads, int reps, int use_ref);
+
 #ifdef __cplusplus
 }
 #endif
