@@ -118,28 +118,42 @@ __device__ __forceinline__ int padded(int m) { return 4 * (m + (m >> 2)); }
 // the chains' reduction runs as DPP row shifts (padded_row_sumsq); otherwise
 // at the natural layout with the lane-exchange reduction, which also covers
 // the leftover 8-float blocks of dim % 32 != 0.
-template <int TPR, int KMAX, bool ADD, int QGS, bool PAD>
+// FIX (with PAD, dim == 4*TPR*KMAX): the row length is the compile-time
+// constant and every chunk is live, so the loads and stores carry no bounds
+// branches (whose merges cost waits on the outstanding loads); the fused-add
+// form then also requests its weights right after the row's loads, ahead of
+// the residual's stores, since vector memory operations retire in issue order
+// and a weight load issued after those stores would wait for them (KMAX <= 4:
+// with more chunks the weights would not fit in 64 VGPRs beside the row).
+template <int TPR, int KMAX, bool ADD, int QGS, bool PAD, bool FIX = false>
 __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *xin, const float *add,
                                         const float *weight, int dim, float eps) {
+  static_assert(!FIX || PAD, "the fixed-length row uses the padded layout");
+  constexpr bool EARLY_W = FIX && ADD && QGS == 0 && KMAX <= 4;
+  if constexpr (FIX) dim = 4 * TPR * KMAX;
   extern __shared__ __attribute__((aligned(16))) float row[];
   const int tid = threadIdx.x;
   const size_t r = blockIdx.x;
   float *xr = xin + r * (size_t)dim;
 
   // Pass 1: load the row (and add), stage it in LDS.
-  float4 x[KMAX], b[KMAX];
+  float4 x[KMAX], b[KMAX], w_early[EARLY_W ? KMAX : 1];
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int i = 4 * (tid + k * TPR);
-    if (i < dim) {
+    if (FIX || i < dim) {
       x[k] = ld_stream4(xr + i);
       if constexpr (ADD) b[k] = ld_stream4(add + r * (size_t)dim + i);
     }
   }
+  if constexpr (EARLY_W) {
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) w_early[k] = *reinterpret_cast<const float4 *>(weight + 4 * (tid + k * TPR));
+  }
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int i = 4 * (tid + k * TPR);
-    if (i < dim) {
+    if (FIX || i < dim) {
       if constexpr (ADD) {
         x[k] = make_float4(x[k].x + b[k].x, x[k].y + b[k].y, x[k].z + b[k].z, x[k].w + b[k].w);
         st_stream4(xr + i, x[k]);
@@ -190,10 +204,14 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int i = 4 * (tid + k * TPR);
-    const bool live = i < dim;
+    const bool live = FIX || i < dim;
     float4 n = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) {
-      const float4 w = *reinterpret_cast<const float4 *>(weight + i);
+      float4 w;
+      if constexpr (EARLY_W)
+        w = w_early[k];
+      else
+        w = *reinterpret_cast<const float4 *>(weight + i);
       n = make_float4((s * x[k].x) * w.x, (s * x[k].y) * w.y, (s * x[k].z) * w.z, (s * x[k].w) * w.w);
     }
     if constexpr (QGS == 0) {
@@ -329,15 +347,15 @@ __global__ __launch_bounds__(TPB ? TPB : 1024) void norm_q8_row16_kernel(int8_t 
   st_stream_f32(q_s + r * (size_t)(dim / QGS) + t / (QGS / 16), scale);
 }
 
-template <int TPR, int KMAX, bool PAD>
+template <int TPR, int KMAX, bool PAD, bool FIX>
 __global__ __launch_bounds__(TPR) void fused_add_rmsnorm_kernel(float *o, float *residual, const float *add,
                                                                 const float *weight, int dim, float eps) {
-  rms_row<TPR, KMAX, true, 0, PAD>(o, nullptr, nullptr, residual, add, weight, dim, eps);
+  rms_row<TPR, KMAX, true, 0, PAD, FIX>(o, nullptr, nullptr, residual, add, weight, dim, eps);
 }
 
-template <int TPR, int KMAX, bool PAD>
+template <int TPR, int KMAX, bool PAD, bool FIX>
 __global__ __launch_bounds__(TPR) void rmsnorm_kernel(float *o, float *x, const float *weight, int dim, float eps) {
-  rms_row<TPR, KMAX, false, 0, PAD>(o, nullptr, nullptr, x, nullptr, weight, dim, eps);
+  rms_row<TPR, KMAX, false, 0, PAD, FIX>(o, nullptr, nullptr, x, nullptr, weight, dim, eps);
 }
 
 template <int TPR, int KMAX, int QGS, bool PAD>
@@ -360,6 +378,8 @@ struct RowLaunch {
   hipStream_t stream;
   // the padded layout and DPP reduction: whole 32-float blocks, at most 64 KiB of LDS (5 bytes per element)
   bool pad() const { return dim % 32 == 0 && dim <= 12288; }
+  // one float4 chunk per thread and k, all live: the fixed-length kernels
+  bool fits(int tpr, int kmax) const { return pad() && dim == 4 * tpr * kmax; }
   size_t lds() const { return (size_t)(pad() ? dim + dim / 4 : dim) * sizeof(float); }
 };
 
@@ -385,10 +405,12 @@ struct AddNormOp {
     auto go = [&](auto kernel) {
       enqueue(kernel, dim3(L.rows), dim3(TPR), L.lds(), L.stream, o, residual, add, weight, L.dim, eps);
     };
-    if (L.pad())
-      go(fused_add_rmsnorm_kernel<TPR, KMAX, true>);
+    if (L.fits(TPR, KMAX))
+      go(fused_add_rmsnorm_kernel<TPR, KMAX, true, true>);
+    else if (L.pad())
+      go(fused_add_rmsnorm_kernel<TPR, KMAX, true, false>);
     else
-      go(fused_add_rmsnorm_kernel<TPR, KMAX, false>);
+      go(fused_add_rmsnorm_kernel<TPR, KMAX, false, false>);
   }
 };
 
@@ -396,10 +418,12 @@ template <int TPR, int KMAX>
 struct NormOp {
   static void launch(const RowLaunch &L, float *o, float *x, const float *weight, float eps) {
     auto go = [&](auto kernel) { enqueue(kernel, dim3(L.rows), dim3(TPR), L.lds(), L.stream, o, x, weight, L.dim, eps); };
-    if (L.pad())
-      go(rmsnorm_kernel<TPR, KMAX, true>);
+    if (L.fits(TPR, KMAX))
+      go(rmsnorm_kernel<TPR, KMAX, true, true>);
+    else if (L.pad())
+      go(rmsnorm_kernel<TPR, KMAX, true, false>);
     else
-      go(rmsnorm_kernel<TPR, KMAX, false>);
+      go(rmsnorm_kernel<TPR, KMAX, false, false>);
   }
 };
 
