@@ -64,8 +64,8 @@ DOMINANT = "swiglu_q8"
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--seed", type=int, default=5)
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--cpu-tokens", type=int, default=2048)
