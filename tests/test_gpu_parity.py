@@ -165,10 +165,13 @@ def test_rmsnorm_rope_validator_cases(ops, oracle, heads, hd, pos, eps, seed):
     assert np.max(np.abs(host(bt) - d)) < 1e-3
 
 
+@pytest.mark.parametrize("H", [3, 8])
 @pytest.mark.parametrize("hd", [64, 96, 128, 160, 192, 256, 480, 512])
-def test_rmsnorm_rope_head_dims(ops, oracle, hd):
-    """Every head_dim % 32 == 0 in [64, 512] class: register rotation (hd % 64 == 0) and LDS rotation."""
-    T, H = 37, 3
+def test_rmsnorm_rope_head_dims(ops, oracle, hd, H):
+    """Every head_dim % 32 == 0 in [64, 512] class: register rotation (hd % 64 == 0) and LDS rotation.  With
+    8 heads per token, hd 64 and 128 run the wave-uniform kernel (37 x 8 heads: the last workgroup's last
+    three waves hold no head)."""
+    T = 37
     buf = C.normal(hd, (T, H, hd))
     w = C.norm_weight(hd + 1, hd)
     ct, st = oracle.rope_tables(64, hd, 1e6)
@@ -177,7 +180,7 @@ def test_rmsnorm_rope_head_dims(ops, oracle, hd):
     want = oracle.rmsnorm_rope(buf, w, ct, st, pos, 1e-6)
     bt = dev(buf)
     ops.rmsnorm_rope_heads(bt, dev(w), dev(ct), dev(st), positions=dev(pos), eps=1e-6)
-    assert_bits(host(bt), want, f"rope hd={hd}")
+    assert_bits(host(bt), want, f"rope hd={hd} H={H}")
 
 
 def test_qk_rmsnorm_rope_config2(ops, oracle):
@@ -202,8 +205,9 @@ def test_qk_rmsnorm_rope_config2(ops, oracle):
     assert_bits(out[:, (Hq + Hk) * D:], qkv[:, (Hq + Hk) * D:], "v untouched")
 
 
-def test_rope_position_outside_tables_gives_nan(ops, oracle):
-    buf = C.normal(9, (3, 2, 64))
+@pytest.mark.parametrize("H", [2, 8])
+def test_rope_position_outside_tables_gives_nan(ops, oracle, H):
+    buf = C.normal(9, (3, H, 64))
     w = C.norm_weight(10, 64)
     ct, st = oracle.rope_tables(8, 64, 1e4)
     pos = np.array([3, 8, 0], np.int32)  # 8 is past the 8-row tables
@@ -532,11 +536,13 @@ def test_kv_pack_f16_kv_one_launch(ops, oracle, rows, kv_dim, q_dim, cache_strid
     assert np.array_equal(host(d), qkv)
 
 
+@pytest.mark.parametrize("heads", [(8, 2), (16, 8)])
 @pytest.mark.parametrize("keep", [True, False])
 @pytest.mark.parametrize("hd", [128, 96])
-def test_qk_rope_with_fused_k_pack(ops, oracle, keep, hd):
+def test_qk_rope_with_fused_k_pack(ops, oracle, keep, hd, heads):
     """RMSNorm+RoPE of Q and K plus the binary16 K cache rows in one launch == RoPE, then v7s_kv_pack_f16 of K."""
-    T, Hq, Hk = 67, 8, 2
+    T = 67
+    Hq, Hk = heads
     qkv = C.normal(hd + 5, (T, (Hq + 2 * Hk) * hd))
     qw = C.norm_weight(hd + 6, hd)
     kw = C.norm_weight(hd + 7, hd)
@@ -562,25 +568,29 @@ def test_qk_rope_with_fused_k_pack(ops, oracle, keep, hd):
 
 # --------------------------------------------------------------------------- RoPE only, the fused Q/K/V stage
 
+@pytest.mark.parametrize("H", [3, 8])
 @pytest.mark.parametrize("hd", [64, 96, 128, 256])
-def test_rope_only_heads_tokens(ops, oracle, hd):
-    T, H = 41, 3
+def test_rope_only_heads_tokens(ops, oracle, hd, H):
+    T = 41
     buf = C.normal(hd + 40, (T, H, hd))
     ct, st = oracle.rope_tables(64, hd, 1e4)
     pos = C.rng(hd).integers(0, 64, T).astype(np.int32)
     pos[0] = 0
     bt = dev(buf)
     ops.rope_only_heads(bt, dev(ct), dev(st), positions=dev(pos))
-    assert_bits(host(bt), oracle.rope_only(buf, ct, st, pos), f"rope only hd={hd}")
+    assert_bits(host(bt), oracle.rope_only(buf, ct, st, pos), f"rope only hd={hd} H={H}")
 
 
+@pytest.mark.parametrize("heads", [(6, 2), (16, 8)])
 @pytest.mark.parametrize("norm", [True, False])
 @pytest.mark.parametrize("bias", [True, False])
 @pytest.mark.parametrize("hd", [128, 96])
-def test_qkv_stage_matches_the_per_token_calls(ops, oracle, norm, bias, hd):
+def test_qkv_stage_matches_the_per_token_calls(ops, oracle, norm, bias, hd, heads):
     """One launch == Stage C of the Q8 prefill per token (src/asm/prefill_q8.inc:848-883): bias add, Q/K
-    RMSNorm+RoPE (Qwen3) or RoPE only (Llama), K and V binary16 cache rows."""
-    T, Hq, Hk = 53, 6, 2
+    RMSNorm+RoPE (Qwen3) or RoPE only (Llama), K and V binary16 cache rows.  16 + 8 + 8 heads of 128 run
+    the wave-uniform kernel."""
+    T = 53
+    Hq, Hk = heads
     w = (Hq + 2 * Hk) * hd
     qkv = C.normal(hd + 90, (T, w))
     qw, kw = C.norm_weight(hd + 91, hd), C.norm_weight(hd + 92, hd)
@@ -613,8 +623,10 @@ def test_qkv_stage_matches_the_per_token_calls(ops, oracle, norm, bias, hd):
     assert_bits(host(vc).view(np.uint16), wvc, "v cache")
 
 
-def test_qkv_stage_cache_only_leaves_f32_k_v(ops, oracle):
-    T, Hq, Hk, hd = 9, 4, 2, 128
+@pytest.mark.parametrize("heads", [(4, 2), (8, 8)])
+def test_qkv_stage_cache_only_leaves_f32_k_v(ops, oracle, heads):
+    T, hd = 9, 128
+    Hq, Hk = heads
     qkv = C.normal(7, (T, (Hq + 2 * Hk) * hd))
     ct, st = oracle.rope_tables(T, hd, 1e6)
     pos = np.arange(T, dtype=np.int32)

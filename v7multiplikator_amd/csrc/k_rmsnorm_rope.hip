@@ -243,8 +243,118 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
   if (hr.live) store_head<K>(hr, xn);
 }
 
+// Zeros that stand in for a missing norm weight or cos/sin row, so that every
+// lane issues the same loads (the results are not used).  K <= 4 reads at
+// most float 4*7 + 32*3 + 3.
+__device__ float kZeroRow[128] = {};  // never written; not const, so it stays in the global address space
+
+// head_dim 64 or 128 when every wave's 8 heads belong to one token and one
+// side (heads per token and the side boundaries are multiples of 8; checked
+// by the launcher): the head's side, its descriptor fields and the position
+// are read once per wave with scalar loads, instead of per lane from the
+// kernel arguments with vector loads, whose in-order completion made every
+// lane wait for its head's data before it could even request the norm
+// weights, and again before the cos/sin rows.  Here a lane's head, weight and
+// cos/sin loads are all in flight together (a side without weights or
+// rotation reads kZeroRow instead); the arithmetic is rmsnorm_rope_reg_kernel's.
+// At most 64 VGPRs: 8 waves per SIMD.
+template <int K>
+__global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave_kernel(RopeArgs a) {
+  static_assert(K == 2 || K == 4, "head_dim 64 or 128");
+  constexpr int KH = K / 2;
+  const int m = threadIdx.x & 7;
+  const unsigned f0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 256u + threadIdx.x) >> 3);  // the wave's first head
+  const bool live = f0 < a.n_heads;  // n_heads is a multiple of 8: the whole wave or none
+  const unsigned ff0 = live ? f0 : 0u;
+  const unsigned t = ff0 / (unsigned)a.heads_per_token;
+  const int h0 = (int)(ff0 - t * (unsigned)a.heads_per_token);
+  const int sd = h0 < a.n_heads0 ? 0 : (h0 < a.n_heads01 ? 1 : 2);
+  const int hs = h0 - (sd == 0 ? 0 : (sd == 1 ? a.n_heads0 : a.n_heads01)) + ((threadIdx.x & 63) >> 3);
+  const RopeSide &S = a.side[sd];
+  const size_t in_head = (size_t)hs * a.head_dim + 4 * m;
+  float *x = S.buf + (size_t)t * (size_t)S.token_stride + in_head;
+  int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
+  // A position outside the tables cannot be read: its rotated heads become NaN.
+  const bool bad_pos = S.rotate && pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
+  if (bad_pos) pos = 0;
+  const bool rot = S.rotate && pos != 0;
+  const size_t row = (size_t)pos * (size_t)a.rope_max_dim + 4 * m;
+  const float *wp = S.norm_weight ? S.norm_weight + 4 * m : kZeroRow + 4 * m;
+  const float *cp = rot ? a.cos_table + row : kZeroRow + 4 * m;
+  const float *sp = rot ? a.sin_table + row : kZeroRow + 4 * m;
+  float4 xv[K], wv[K], c[KH], sn[KH];
+#pragma unroll
+  for (int k = 0; k < K; ++k) xv[k] = ld_stream4(x + 32 * k);
+#pragma unroll
+  for (int k = 0; k < K; ++k) wv[k] = *reinterpret_cast<const float4 *>(wp + 32 * k);
+#pragma unroll
+  for (int k = 0; k < KH; ++k) {
+    c[k] = *reinterpret_cast<const float4 *>(cp + 32 * k);
+    sn[k] = *reinterpret_cast<const float4 *>(sp + 32 * k);
+  }
+  // The loads above are issued here, ahead of the branches below (the
+  // compiler would otherwise sink the weight and table loads past them).
+  asm volatile("" ::: "memory");
+  if (S.bias) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float4 b = *reinterpret_cast<const float4 *>(S.bias + in_head + 32 * k);
+      xv[k] = make_float4(xv[k].x + b.x, xv[k].y + b.y, xv[k].z + b.z, xv[k].w + b.w);
+    }
+  }
+  float4 xn[K];
+  if (S.norm_weight) {
+    const float s = head_scale<K>(xv, 32 * K, a.eps);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      xn[k] = make_float4((xv[k].x * s) * wv[k].x, (xv[k].y * s) * wv[k].y, (xv[k].z * s) * wv[k].z,
+                          (xv[k].w * s) * wv[k].w);
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) xn[k] = xv[k];
+  }
+  if (bad_pos) {
+    const float q = __builtin_nanf("");
+#pragma unroll
+    for (int k = 0; k < K; ++k) xn[k] = make_float4(q, q, q, q);
+  }
+  if (rot) {
+#pragma unroll
+    for (int k = 0; k < KH; ++k) {
+      const float4 ev = xn[k], od = xn[k + KH];
+      xn[k] = make_float4(__builtin_fmaf(-od.x, sn[k].x, ev.x * c[k].x), __builtin_fmaf(-od.y, sn[k].y, ev.y * c[k].y),
+                          __builtin_fmaf(-od.z, sn[k].z, ev.z * c[k].z), __builtin_fmaf(-od.w, sn[k].w, ev.w * c[k].w));
+      xn[k + KH] = make_float4(__builtin_fmaf(od.x, c[k].x, ev.x * sn[k].x), __builtin_fmaf(od.y, c[k].y, ev.y * sn[k].y),
+                               __builtin_fmaf(od.z, c[k].z, ev.z * sn[k].z), __builtin_fmaf(od.w, c[k].w, ev.w * sn[k].w));
+    }
+  }
+  if (live) {
+    if (!S.cache || S.keep_f32) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) st_stream4(x + 32 * k, xn[k]);
+    }
+    if (S.cache) {
+      uint16_t *kc = S.cache + (size_t)t * (size_t)S.cache_stride + in_head;
+#pragma unroll
+      for (int k = 0; k < K; ++k) st_stream_u2(reinterpret_cast<uint32_t *>(kc + 32 * k), pack4_f16(xn[k]));
+    }
+  }
+}
+
+// Every wave's 8 consecutive heads (flat over tokens x sides) lie in one token
+// and one side.
+static bool wave_uniform_sides(const RopeArgs &a) {
+  return a.heads_per_token % 8 == 0 && a.n_heads0 % 8 == 0 && a.n_heads01 % 8 == 0;
+}
+
 template <int K>
 static void launch_k(const RopeArgs &a, hipStream_t stream) {
+  if constexpr (K == 2 || K == 4) {
+    if (wave_uniform_sides(a)) {
+      enqueue((rmsnorm_rope_wave_kernel<K>), dim3((a.n_heads + 31u) / 32u), dim3(256), 0, stream, a);
+      return;
+    }
+  }
   if ((32 * K) % 64 == 0) {
     constexpr int HPU = 1;
     const unsigned units = (a.n_heads + HPU - 1) / HPU;
