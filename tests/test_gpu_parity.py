@@ -205,6 +205,28 @@ def test_qk_rmsnorm_rope_config2(ops, oracle):
     assert_bits(out[:, (Hq + Hk) * D:], qkv[:, (Hq + Hk) * D:], "v untouched")
 
 
+@pytest.mark.parametrize("Hq,Hk,D", [(28, 4, 128), (14, 2, 64), (12, 2, 64)])
+def test_qk_rmsnorm_rope_partial_waves(ops, oracle, Hq, Hk, D):
+    """Head counts that are not multiples of 8 (Qwen2.5-style 28 + 4, 14 + 2, 12 + 2): the wave kernel's
+    last wave of each side holds fewer than 8 heads; its spare lanes must store nothing."""
+    T = 37
+    qkv = C.normal(Hq * 100 + Hk, (T, (Hq + 2 * Hk) * D))
+    qw, kw = C.norm_weight(Hq + 1, D), C.norm_weight(Hk + 2, D)
+    ct, st = oracle.rope_tables(64, D, 1e6)
+    pos = C.rng(Hq).integers(0, 64, T).astype(np.int32)
+    pos[5] = 0
+    q_np = qkv[:, :Hq * D].reshape(T, Hq, D)
+    k_np = qkv[:, Hq * D:(Hq + Hk) * D].reshape(T, Hk, D)
+    t = dev(qkv)
+    q = t[:, :Hq * D].view(T, Hq, D)
+    k = t[:, Hq * D:(Hq + Hk) * D].view(T, Hk, D)
+    ops.qk_rmsnorm_rope(q, k, dev(qw), dev(kw), dev(ct), dev(st), positions=dev(pos), eps=1e-6)
+    out = host(t)
+    assert_bits(out[:, :Hq * D].reshape(T, Hq, D), oracle.rmsnorm_rope(q_np, qw, ct, st, pos, 1e-6), "q")
+    assert_bits(out[:, Hq * D:(Hq + Hk) * D].reshape(T, Hk, D), oracle.rmsnorm_rope(k_np, kw, ct, st, pos, 1e-6), "k")
+    assert_bits(out[:, (Hq + Hk) * D:], qkv[:, (Hq + Hk) * D:], "v untouched")
+
+
 @pytest.mark.parametrize("H", [2, 8])
 def test_rope_position_outside_tables_gives_nan(ops, oracle, H):
     buf = C.normal(9, (3, H, 64))

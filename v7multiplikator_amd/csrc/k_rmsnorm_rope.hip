@@ -40,6 +40,10 @@ struct RopeArgs {
   int n_heads0, n_heads01;  // side 0 heads; sides 0 + 1 heads
   int heads_per_token;      // heads of all sides
   unsigned n_heads;         // n_tokens * heads_per_token
+  // The wave kernel's grid: per token, ceil(heads / 8) waves for each side.
+  int wave0, wave01;        // side 0 waves; sides 0 + 1 waves
+  int waves_per_token;
+  unsigned n_waves;         // n_tokens * waves_per_token
   int head_dim;
   const float *cos_table;
   const float *sin_table;
@@ -248,29 +252,32 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
 // most float 4*7 + 32*3 + 3.
 __device__ float kZeroRow[128] = {};  // never written; not const, so it stays in the global address space
 
-// head_dim 64 or 128 when every wave's 8 heads belong to one token and one
-// side (heads per token and the side boundaries are multiples of 8; checked
-// by the launcher): the head's side, its descriptor fields and the position
-// are read once per wave with scalar loads, instead of per lane from the
-// kernel arguments with vector loads, whose in-order completion made every
-// lane wait for its head's data before it could even request the norm
-// weights, and again before the cos/sin rows.  Here a lane's head, weight and
-// cos/sin loads are all in flight together (a side without weights or
-// rotation reads kZeroRow instead); the arithmetic is rmsnorm_rope_reg_kernel's.
-// At most 64 VGPRs: 8 waves per SIMD.
+// head_dim 64 or 128: each wave takes up to 8 heads of one side of one token
+// (ceil(heads / 8) waves per side and token), so the side, its descriptor
+// fields and the position are read once per wave with scalar loads, instead
+// of per lane from the kernel arguments with vector loads, whose in-order
+// completion made every lane wait for its head's data before it could even
+// request the norm weights, and again before the cos/sin rows.  Here a lane's
+// head, weight and cos/sin loads are all in flight together (a side without
+// weights or rotation reads kZeroRow instead).  Lanes past the side's last
+// head repeat that head's loads, which the same instructions fetch anyway, and
+// store nothing.  The arithmetic is rmsnorm_rope_reg_kernel's.  At most 64
+// VGPRs: 8 waves per SIMD.
 template <int K>
 __global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave_kernel(RopeArgs a) {
   static_assert(K == 2 || K == 4, "head_dim 64 or 128");
   constexpr int KH = K / 2;
   const int m = threadIdx.x & 7;
-  const unsigned f0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 256u + threadIdx.x) >> 3);  // the wave's first head
-  const bool live = f0 < a.n_heads;  // n_heads is a multiple of 8: the whole wave or none
-  const unsigned ff0 = live ? f0 : 0u;
-  const unsigned t = ff0 / (unsigned)a.heads_per_token;
-  const int h0 = (int)(ff0 - t * (unsigned)a.heads_per_token);
-  const int sd = h0 < a.n_heads0 ? 0 : (h0 < a.n_heads01 ? 1 : 2);
-  const int hs = h0 - (sd == 0 ? 0 : (sd == 1 ? a.n_heads0 : a.n_heads01)) + ((threadIdx.x & 63) >> 3);
+  const unsigned wi = __builtin_amdgcn_readfirstlane((blockIdx.x * 256u + threadIdx.x) >> 6);  // wave index
+  const bool live_wave = wi < a.n_waves;
+  const unsigned wvv = live_wave ? wi : 0u;
+  const unsigned t = wvv / (unsigned)a.waves_per_token;
+  const int r = (int)(wvv - t * (unsigned)a.waves_per_token);
+  const int sd = r < a.wave0 ? 0 : (r < a.wave01 ? 1 : 2);
   const RopeSide &S = a.side[sd];
+  const int hs_raw = 8 * (r - (sd == 0 ? 0 : (sd == 1 ? a.wave0 : a.wave01))) + ((threadIdx.x & 63) >> 3);
+  const bool live = live_wave && hs_raw < S.n_heads;
+  const int hs = hs_raw < S.n_heads ? hs_raw : S.n_heads - 1;
   const size_t in_head = (size_t)hs * a.head_dim + 4 * m;
   float *x = S.buf + (size_t)t * (size_t)S.token_stride + in_head;
   int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
@@ -341,17 +348,12 @@ __global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave_kernel(RopeArgs a) {
   }
 }
 
-// Every wave's 8 consecutive heads (flat over tokens x sides) lie in one token
-// and one side.
-static bool wave_uniform_sides(const RopeArgs &a) {
-  return a.heads_per_token % 8 == 0 && a.n_heads0 % 8 == 0 && a.n_heads01 % 8 == 0;
-}
-
 template <int K>
 static void launch_k(const RopeArgs &a, hipStream_t stream) {
   if constexpr (K == 2 || K == 4) {
-    if (wave_uniform_sides(a)) {
-      enqueue((rmsnorm_rope_wave_kernel<K>), dim3((a.n_heads + 31u) / 32u), dim3(256), 0, stream, a);
+    // 64 threads per wave index in 32 bits: n_waves < 2^26 (the general kernel covers the rest)
+    if (a.n_waves < (1u << 26)) {
+      enqueue((rmsnorm_rope_wave_kernel<K>), dim3((a.n_waves + 3u) / 4u), dim3(256), 0, stream, a);
       return;
     }
   }
@@ -374,6 +376,12 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.n_heads01 = a.n_heads0 + (n_sides > 1 ? sides[1].n_heads : 0);
   a.heads_per_token = a.n_heads01 + (n_sides > 2 ? sides[2].n_heads : 0);
   a.n_heads = (unsigned)n_tokens * (unsigned)a.heads_per_token;
+  auto waves = [&](int i) { return i < n_sides ? (sides[i].n_heads + 7) / 8 : 0; };
+  a.wave0 = waves(0);
+  a.wave01 = a.wave0 + waves(1);
+  a.waves_per_token = a.wave01 + waves(2);
+  const unsigned long long n_waves = (unsigned long long)n_tokens * (unsigned long long)a.waves_per_token;
+  a.n_waves = n_waves < (1ull << 26) ? (unsigned)n_waves : (1u << 26);  // beyond: the general kernel
   a.head_dim = head_dim;
   a.cos_table = cos_table;
   a.sin_table = sin_table;
