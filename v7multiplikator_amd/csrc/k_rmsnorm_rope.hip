@@ -248,11 +248,11 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
 }
 
 // Zeros that stand in for a missing norm weight or cos/sin row, so that every
-// lane issues the same loads (the results are not used).  K <= 4 reads at
-// most float 4*7 + 32*3 + 3.
-__device__ float kZeroRow[128] = {};  // never written; not const, so it stays in the global address space
+// lane issues the same loads (the results are not used).  K <= 8 reads at
+// most float 4*7 + 32*7 + 3.
+__device__ float kZeroRow[256] = {};  // never written; not const, so it stays in the global address space
 
-// head_dim 64 or 128: each wave takes up to 8 heads of one side of one token
+// head_dim 64, 128, 192 or 256: each wave takes up to 8 heads of one side of one token
 // (ceil(heads / 8) waves per side and token), so the side, its descriptor
 // fields and the position are read once per wave with scalar loads, instead
 // of per lane from the kernel arguments with vector loads, whose in-order
@@ -262,10 +262,11 @@ __device__ float kZeroRow[128] = {};  // never written; not const, so it stays i
 // weights or rotation reads kZeroRow instead).  Lanes past the side's last
 // head repeat that head's loads, which the same instructions fetch anyway, and
 // store nothing.  The arithmetic is rmsnorm_rope_reg_kernel's.  At most 64
-// VGPRs: 8 waves per SIMD.
+// VGPRs (8 waves per SIMD) up to head_dim 128; 104-110 at 192 and 256, where
+// having every load in flight still beats the per-lane kernel's occupancy.
 template <int K>
-__global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave_kernel(RopeArgs a) {
-  static_assert(K == 2 || K == 4, "head_dim 64 or 128");
+__global__ __launch_bounds__(256, K <= 4 ? 8 : 1) void rmsnorm_rope_wave_kernel(RopeArgs a) {
+  static_assert(K % 2 == 0 && K <= 8, "head_dim 64, 128, 192 or 256");
   constexpr int KH = K / 2;
   const int m = threadIdx.x & 7;
   const unsigned wi = __builtin_amdgcn_readfirstlane((blockIdx.x * 256u + threadIdx.x) >> 6);  // wave index
@@ -350,7 +351,7 @@ __global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave_kernel(RopeArgs a) {
 
 template <int K>
 static void launch_k(const RopeArgs &a, hipStream_t stream) {
-  if constexpr (K == 2 || K == 4) {
+  if constexpr (K % 2 == 0 && K <= 8) {
     // 64 threads per wave index in 32 bits: n_waves < 2^26 (the general kernel covers the rest)
     if (a.n_waves < (1u << 26)) {
       enqueue((rmsnorm_rope_wave_kernel<K>), dim3((a.n_waves + 3u) / 4u), dim3(256), 0, stream, a);
