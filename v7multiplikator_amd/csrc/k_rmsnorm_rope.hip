@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
 // most float 4*7 + 32*7 + 3.
 __device__ float kZeroRow[256] = {};  // never written; not const, so it stays in the global address space
 
-// head_dim 64, 128, 192 or 256: each wave takes up to 8 heads of one side of one token
+// head_dim 64 to 256: each wave takes up to 8 heads of one side of one token
 // (ceil(heads / 8) waves per side and token), so the side, its descriptor
 // fields and the position are read once per wave with scalar loads, instead
 // of per lane from the kernel arguments with vector loads, whose in-order
@@ -264,11 +264,23 @@ __device__ float kZeroRow[256] = {};  // never written; not const, so it stays i
 // store nothing.  The arithmetic is rmsnorm_rope_reg_kernel's.  At most 64
 // VGPRs (8 waves per SIMD) up to head_dim 128; 104-110 at 192 and 256, where
 // having every load in flight still beats the per-lane kernel's occupancy.
+//
+// head_dim % 64 == 32 (odd K): the rotate-half partner of lane m's block k is
+// in lane m ^ 4 of the same head, in block k + J (k - J - 1) for lanes 0..3
+// and k + J + 1 (k - J) for lanes 4..7 in the first (second) half, J = (K-1)/2;
+// each lane sends the block its partner needs (a per-lane choice between two
+// compile-time blocks) through one xor-4 exchange per block, and loads the
+// cos/sin entries of its own elements (j = e in the first half, e - hd/2 in
+// the second).
 template <int K>
-__global__ __launch_bounds__(256, K <= 4 ? 8 : 1) void rmsnorm_rope_wave_kernel(RopeArgs a) {
-  static_assert(K % 2 == 0 && K <= 8, "head_dim 64, 128, 192 or 256");
-  constexpr int KH = K / 2;
+__global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rmsnorm_rope_wave_kernel(RopeArgs a) {
+  static_assert(K >= 2 && K <= 8, "head_dim 64 to 256");
+  constexpr bool ODD = K % 2 == 1;
+  constexpr int KH = K / 2;         // even K: the partner of block k is block k + KH in the same lane
+  constexpr int KC = ODD ? K : KH;  // cos/sin float4 per lane
+  constexpr int J = (K - 1) / 2;
   const int m = threadIdx.x & 7;
+  const bool lo = m < 4;
   const unsigned wi = __builtin_amdgcn_readfirstlane((blockIdx.x * 256u + threadIdx.x) >> 6);  // wave index
   const bool live_wave = wi < a.n_waves;
   const unsigned wvv = live_wave ? wi : 0u;
@@ -290,15 +302,18 @@ __global__ __launch_bounds__(256, K <= 4 ? 8 : 1) void rmsnorm_rope_wave_kernel(
   const float *wp = S.norm_weight ? S.norm_weight + 4 * m : kZeroRow + 4 * m;
   const float *cp = rot ? a.cos_table + row : kZeroRow + 4 * m;
   const float *sp = rot ? a.sin_table + row : kZeroRow + 4 * m;
-  float4 xv[K], wv[K], c[KH], sn[KH];
+  // odd K: whether the lane's block k lies in the first half of the head
+  auto first_half = [&](int k) { return lo ? k <= J : k < J; };
+  float4 xv[K], wv[K], c[KC], sn[KC];
 #pragma unroll
   for (int k = 0; k < K; ++k) xv[k] = ld_stream4(x + 32 * k);
 #pragma unroll
   for (int k = 0; k < K; ++k) wv[k] = *reinterpret_cast<const float4 *>(wp + 32 * k);
 #pragma unroll
-  for (int k = 0; k < KH; ++k) {
-    c[k] = *reinterpret_cast<const float4 *>(cp + 32 * k);
-    sn[k] = *reinterpret_cast<const float4 *>(sp + 32 * k);
+  for (int k = 0; k < KC; ++k) {
+    const int off = (!ODD || first_half(k)) ? 32 * k : 32 * k - 16 * K;
+    c[k] = *reinterpret_cast<const float4 *>(cp + off);
+    sn[k] = *reinterpret_cast<const float4 *>(sp + off);
   }
   // The loads above are issued here, ahead of the branches below (the
   // compiler would otherwise sink the weight and table loads past them).
@@ -326,7 +341,7 @@ __global__ __launch_bounds__(256, K <= 4 ? 8 : 1) void rmsnorm_rope_wave_kernel(
 #pragma unroll
     for (int k = 0; k < K; ++k) xn[k] = make_float4(q, q, q, q);
   }
-  if (rot) {
+  if (rot && !ODD) {
 #pragma unroll
     for (int k = 0; k < KH; ++k) {
       const float4 ev = xn[k], od = xn[k + KH];
@@ -334,6 +349,27 @@ __global__ __launch_bounds__(256, K <= 4 ? 8 : 1) void rmsnorm_rope_wave_kernel(
                           __builtin_fmaf(-od.z, sn[k].z, ev.z * c[k].z), __builtin_fmaf(-od.w, sn[k].w, ev.w * c[k].w));
       xn[k + KH] = make_float4(__builtin_fmaf(od.x, c[k].x, ev.x * sn[k].x), __builtin_fmaf(od.y, c[k].y, ev.y * sn[k].y),
                                __builtin_fmaf(od.z, c[k].z, ev.z * sn[k].z), __builtin_fmaf(od.w, c[k].w, ev.w * sn[k].w));
+    }
+  }
+  if (rot && ODD) {  // rot is uniform over the wave: every lane takes part in the exchanges
+    float4 part[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      // the block this lane's partner (lane m ^ 4, in the other half of the 8 lanes) needs for its block k
+      const int kp_for_lo = k <= J ? k + J : k - J - 1;      // partner in lanes 0..3
+      const int kp_for_hi = k <= J - 1 ? k + J + 1 : k - J;  // partner in lanes 4..7
+      const float4 snd = lo ? xn[kp_for_hi] : xn[kp_for_lo];
+      part[k] = make_float4(xor_f(snd.x, 4), xor_f(snd.y, 4), xor_f(snd.z, 4), xor_f(snd.w, 4));
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float4 me = xn[k], pa = part[k];
+      if (first_half(k))  // me = x_j, partner = x_{j+h}
+        xn[k] = make_float4(__builtin_fmaf(-pa.x, sn[k].x, me.x * c[k].x), __builtin_fmaf(-pa.y, sn[k].y, me.y * c[k].y),
+                            __builtin_fmaf(-pa.z, sn[k].z, me.z * c[k].z), __builtin_fmaf(-pa.w, sn[k].w, me.w * c[k].w));
+      else  // me = x_{j+h}, partner = x_j
+        xn[k] = make_float4(__builtin_fmaf(me.x, c[k].x, pa.x * sn[k].x), __builtin_fmaf(me.y, c[k].y, pa.y * sn[k].y),
+                            __builtin_fmaf(me.z, c[k].z, pa.z * sn[k].z), __builtin_fmaf(me.w, c[k].w, pa.w * sn[k].w));
     }
   }
   if (live) {
@@ -351,7 +387,7 @@ __global__ __launch_bounds__(256, K <= 4 ? 8 : 1) void rmsnorm_rope_wave_kernel(
 
 template <int K>
 static void launch_k(const RopeArgs &a, hipStream_t stream) {
-  if constexpr (K % 2 == 0 && K <= 8) {
+  if constexpr (K <= 8) {
     // 64 threads per wave index in 32 bits: n_waves < 2^26 (the general kernel covers the rest)
     if (a.n_waves < (1u << 26)) {
       enqueue((rmsnorm_rope_wave_kernel<K>), dim3((a.n_waves + 3u) / 4u), dim3(256), 0, stream, a);
