@@ -27,6 +27,11 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
     "-fgpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # The first kernel-argument dwords arrive in SGPRs at wave launch instead of
+    # through a scalar load and its wait at the start of every wave (the code
+    # keeps a prologue that loads them itself where the firmware does not
+    # preload).
+    "-mllvm", "-amdgpu-kernarg-preload-count=14",
     "-Wall", "-Wno-unused-function",
 ]
 
