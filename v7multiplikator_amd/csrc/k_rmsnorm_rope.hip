@@ -262,8 +262,8 @@ __device__ float kZeroRow[256] = {};  // never written; not const, so it stays i
 // weights or rotation reads kZeroRow instead).  Lanes past the side's last
 // head repeat that head's loads, which the same instructions fetch anyway, and
 // store nothing.  The arithmetic is rmsnorm_rope_reg_kernel's.  At most 64
-// VGPRs (8 waves per SIMD) up to head_dim 128; 104-110 at 192 and 256, where
-// having every load in flight still beats the per-lane kernel's occupancy.
+// VGPRs (8 waves per SIMD) up to head_dim 128; 104-127 from 160 to 256, where
+// having every load in flight still beats the per-lane kernels' occupancy.
 //
 // head_dim % 64 == 32 (odd K): the rotate-half partner of lane m's block k is
 // in lane m ^ 4 of the same head, in block k + J (k - J - 1) for lanes 0..3
