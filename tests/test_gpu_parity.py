@@ -114,6 +114,28 @@ def test_fused_add_rmsnorm_validator_shapes(ops, oracle, dim, seed):
         assert_bits(host(got_o), want_o, "o")
 
 
+# Model widths: each compiled-in shape of the fixed-length row (2560, 3072, 3584, 3840, 5120, 8192), the run-time
+# thread count with 1, 2 and 4 chunks per thread (1280, 1536 / 6144, 7168 / none below 8192 beyond those), the
+# dispatch shapes (2048, 4096) and a multiple of 256 that falls back to the general kernel (4352).
+MODEL_WIDTHS = [1280, 1536, 2048, 2560, 3072, 3584, 3840, 4096, 4352, 5120, 6144, 7168, 8192]
+
+
+@pytest.mark.parametrize("dim", MODEL_WIDTHS)
+def test_fused_add_rmsnorm_model_widths(ops, oracle, dim):
+    rows = 37
+    r = C.normal(dim, (rows, dim))
+    a = C.normal(dim + 1, (rows, dim))
+    w = C.norm_weight(dim + 2, dim)
+    want_o, want_r = oracle.fused_add_rmsnorm(r, a, w, 1e-6)
+    rt = dev(r)
+    got_o = ops.fused_add_rmsnorm(rt, dev(a), dev(w), eps=1e-6)
+    assert_bits(host(rt), want_r, f"residual dim={dim}")
+    assert_bits(host(got_o), want_o, f"o dim={dim}")
+    rt = dev(r)
+    ops.fused_add_rmsnorm(rt, dev(a), dev(w), eps=1e-6, out=rt)
+    assert_bits(host(rt), want_o, f"in-place o dim={dim}")
+
+
 def test_fused_add_rmsnorm_out_aliases_residual(ops, oracle):
     r = C.normal(5, (64, 2048))
     a = C.normal(6, (64, 2048))
@@ -459,6 +481,18 @@ def test_rmsnorm_rows(ops, oracle, dim, seed):
     xt = dev(x)
     ops.rmsnorm(xt, dev(w), out=xt)  # in place
     assert_bits(host(xt), oracle.rmsnorm(x, w, 1e-6), "rmsnorm in place")
+
+
+@pytest.mark.parametrize("dim", MODEL_WIDTHS)
+def test_rmsnorm_model_widths(ops, oracle, dim):
+    rows = 37
+    x = C.normal(dim + 3, (rows, dim), 2.0)
+    w = C.norm_weight(dim + 4, dim)
+    want = oracle.rmsnorm(x, w, 1e-5)
+    assert_bits(host(ops.rmsnorm(dev(x), dev(w), eps=1e-5)), want, f"rmsnorm dim={dim}")
+    xt = dev(x)
+    ops.rmsnorm(xt, dev(w), eps=1e-5, out=xt)
+    assert_bits(host(xt), want, f"rmsnorm in place dim={dim}")
 
 
 @pytest.mark.parametrize("gs", [64, 32])

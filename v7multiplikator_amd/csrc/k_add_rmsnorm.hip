@@ -118,19 +118,23 @@ __device__ __forceinline__ int padded(int m) { return 4 * (m + (m >> 2)); }
 // the chains' reduction runs as DPP row shifts (padded_row_sumsq); otherwise
 // at the natural layout with the lane-exchange reduction, which also covers
 // the leftover 8-float blocks of dim % 32 != 0.
-// FIX (with PAD, dim == 4*TPR*KMAX): the row length is the compile-time
-// constant and every chunk is live, so the loads and stores carry no bounds
-// branches (whose merges cost waits on the outstanding loads); the fused-add
-// form then also requests its weights right after the row's loads, ahead of
-// the residual's stores, since vector memory operations retire in issue order
-// and a weight load issued after those stores would wait for them (KMAX <= 4:
-// with more chunks the weights would not fit in 64 VGPRs beside the row).
+// FIX (with PAD, dim == 4*TPR*KMAX): every chunk is live, so the loads and
+// stores carry no bounds branches (whose merges cost waits on the outstanding
+// loads); the fused-add form then also requests its weights right after the
+// row's loads, ahead of the residual's stores, since vector memory operations
+// retire in issue order and a weight load issued after those stores would
+// wait for them (KMAX <= 4: with more chunks the weights would not fit in 64
+// VGPRs beside the row).  TPR == 0 (FIX only): the thread count is the
+// launch's blockDim.x and dim = 4*blockDim.x*KMAX; a compile-time TPR folds
+// the chunk offsets into the instructions and measured about 2% faster.
 template <int TPR, int KMAX, bool ADD, int QGS, bool PAD, bool FIX = false>
 __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *xin, const float *add,
                                         const float *weight, int dim, float eps) {
   static_assert(!FIX || PAD, "the fixed-length row uses the padded layout");
+  static_assert(TPR > 0 || (FIX && QGS == 0), "a run-time thread count only for the fixed-length row");
   constexpr bool EARLY_W = FIX && ADD && QGS == 0 && KMAX <= 4;
-  if constexpr (FIX) dim = 4 * TPR * KMAX;
+  const int tpr = TPR ? TPR : (int)blockDim.x;
+  if constexpr (FIX) dim = 4 * tpr * KMAX;
   extern __shared__ __attribute__((aligned(16))) float row[];
   const int tid = threadIdx.x;
   const size_t r = blockIdx.x;
@@ -140,7 +144,7 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
   float4 x[KMAX], b[KMAX], w_early[EARLY_W ? KMAX : 1];
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
-    const int i = 4 * (tid + k * TPR);
+    const int i = 4 * (tid + k * tpr);
     if (FIX || i < dim) {
       x[k] = ld_stream4(xr + i);
       if constexpr (ADD) b[k] = ld_stream4(add + r * (size_t)dim + i);
@@ -148,17 +152,17 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
   }
   if constexpr (EARLY_W) {
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) w_early[k] = *reinterpret_cast<const float4 *>(weight + 4 * (tid + k * TPR));
+    for (int k = 0; k < KMAX; ++k) w_early[k] = *reinterpret_cast<const float4 *>(weight + 4 * (tid + k * tpr));
   }
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
-    const int i = 4 * (tid + k * TPR);
+    const int i = 4 * (tid + k * tpr);
     if (FIX || i < dim) {
       if constexpr (ADD) {
         x[k] = make_float4(x[k].x + b[k].x, x[k].y + b[k].y, x[k].z + b[k].z, x[k].w + b[k].w);
         st_stream4(xr + i, x[k]);
       }
-      *reinterpret_cast<float4 *>(row + (PAD ? padded(tid + k * TPR) : i)) = x[k];
+      *reinterpret_cast<float4 *>(row + (PAD ? padded(tid + k * tpr) : i)) = x[k];
     }
   }
   __syncthreads();
@@ -203,7 +207,7 @@ __device__ __forceinline__ void rms_row(float *o, int8_t *q, float *q_s, float *
   // Pass 2: n = (s * x) * w, then either stored or quantized.
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
-    const int i = 4 * (tid + k * TPR);
+    const int i = 4 * (tid + k * tpr);
     const bool live = FIX || i < dim;
     float4 n = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) {
@@ -348,13 +352,13 @@ __global__ __launch_bounds__(TPB ? TPB : 1024) void norm_q8_row16_kernel(int8_t 
 }
 
 template <int TPR, int KMAX, bool PAD, bool FIX>
-__global__ __launch_bounds__(TPR) void fused_add_rmsnorm_kernel(float *o, float *residual, const float *add,
+__global__ __launch_bounds__(TPR ? TPR : 1024, (TPR == 0 && KMAX <= 4) ? 8 : 1) void fused_add_rmsnorm_kernel(float *o, float *residual, const float *add,
                                                                 const float *weight, int dim, float eps) {
   rms_row<TPR, KMAX, true, 0, PAD, FIX>(o, nullptr, nullptr, residual, add, weight, dim, eps);
 }
 
 template <int TPR, int KMAX, bool PAD, bool FIX>
-__global__ __launch_bounds__(TPR) void rmsnorm_kernel(float *o, float *x, const float *weight, int dim, float eps) {
+__global__ __launch_bounds__(TPR ? TPR : 1024, (TPR == 0 && KMAX <= 4) ? 8 : 1) void rmsnorm_kernel(float *o, float *x, const float *weight, int dim, float eps) {
   rms_row<TPR, KMAX, false, 0, PAD, FIX>(o, nullptr, nullptr, x, nullptr, weight, dim, eps);
 }
 
@@ -454,13 +458,62 @@ struct NormQ8Op {
   }
 };
 
+template <bool ADD, int TPR, int KMAX>
+static auto fixed_row_kernel() {
+  if constexpr (ADD)
+    return fused_add_rmsnorm_kernel<TPR, KMAX, true, true>;
+  else
+    return rmsnorm_kernel<TPR, KMAX, true, true>;
+}
+
+// The fixed-length row at the widths between and above the powers of two,
+// 1024 < dim <= 8192, dim % 256 == 0 (dim = 4 * threads * chunks): the shape
+// that measured fastest at [8192, dim] for the common model widths, compiled
+// in (2560, 3072, 3584, 3840, 5120, 8192: 1.5 to 2.5 points of the HBM peak
+// above the general kernel, 8192 even); a run-time thread count with 2, 1 or
+// 4 chunks per thread for the other multiples of 256.  2048 and 4096 keep the
+// dispatch_rows shapes, which measured best.  Returns false where none applies.
+template <bool ADD>
+static bool launch_fixed_row(const RowLaunch &L, float *o, float *x, const float *add, const float *weight,
+                             float eps) {
+  if (L.dim <= 1024 || L.dim > 8192 || L.dim % 256 || L.dim == 2048 || L.dim == 4096) return false;
+  auto go = [&](auto kernel, int tpr) {
+    if constexpr (ADD)
+      enqueue(kernel, dim3(L.rows), dim3(tpr), L.lds(), L.stream, o, x, add, weight, L.dim, eps);
+    else
+      enqueue(kernel, dim3(L.rows), dim3(tpr), L.lds(), L.stream, o, x, weight, L.dim, eps);
+  };
+  switch (L.dim) {
+    case 2560: go(fixed_row_kernel<ADD, 320, 2>(), 320); return true;
+    case 3072: go(fixed_row_kernel<ADD, 256, 3>(), 256); return true;
+    case 3584: go(fixed_row_kernel<ADD, 448, 2>(), 448); return true;
+    case 3840: go(fixed_row_kernel<ADD, 960, 1>(), 960); return true;
+    case 5120: go(fixed_row_kernel<ADD, 640, 2>(), 640); return true;
+    case 8192: go(fixed_row_kernel<ADD, 512, 4>(), 512); return true;
+  }
+  const int chunks = L.dim / 4;  // a multiple of 64: whole waves
+  if (chunks % 128 == 0 && chunks / 2 <= 1024)
+    go(fixed_row_kernel<ADD, 0, 2>(), chunks / 2);
+  else if (chunks <= 1024)
+    go(fixed_row_kernel<ADD, 0, 1>(), chunks);
+  else if (chunks % 256 == 0)
+    go(fixed_row_kernel<ADD, 0, 4>(), chunks / 4);
+  else
+    return false;
+  return true;
+}
+
 void launch_fused_add_rmsnorm(float *o, float *residual, const float *add, const float *weight, int rows, int dim,
                               float eps, hipStream_t stream) {
-  dispatch_rows<AddNormOp>(RowLaunch{rows, dim, stream}, o, residual, add, weight, eps);
+  const RowLaunch L{rows, dim, stream};
+  if (!launch_fixed_row<true>(L, o, residual, add, weight, eps))
+    dispatch_rows<AddNormOp>(L, o, residual, add, weight, eps);
 }
 
 void launch_rmsnorm(float *o, const float *x, const float *weight, int rows, int dim, float eps, hipStream_t stream) {
-  dispatch_rows<NormOp>(RowLaunch{rows, dim, stream}, o, const_cast<float *>(x), weight, eps);
+  const RowLaunch L{rows, dim, stream};
+  if (!launch_fixed_row<false>(L, o, const_cast<float *>(x), nullptr, weight, eps))
+    dispatch_rows<NormOp>(L, o, const_cast<float *>(x), weight, eps);
 }
 
 void launch_rmsnorm_quantize(int8_t *q, float *q_s, float *x, const float *add, const float *weight, int rows,

@@ -14,8 +14,10 @@
 //   v7g_loadtest <libv7g.so> kv_pack <tokens> <kv_dim>       (two launches, one per side)
 //   v7g_loadtest <libv7g.so> kv_pack_kv <tokens> <kv_dim>    (K and V in one launch)
 //   v7g_loadtest <libv7g.so> qkv_stage <tokens> <q_heads> <kv_heads> <head_dim>
+//   v7g_loadtest <libv7g.so> rope_only <tokens> <q_heads> <kv_heads> <head_dim> [bias 0|1]
 //   v7g_loadtest <libv7g.so> configs          (every benchmark configuration below)
 //   v7g_loadtest <libv7g.so> next             (the widened rows at the Qwen3-8B T=8192 shape)
+//   v7g_loadtest <libv7g.so> models [tokens] [name]  (the per-layer kernels at other model shapes)
 //   options: --iterations N  --time secs  --no-rotate  --per-row
 //
 // Like the reference harnesses it loads the library with dlopen and resolves
@@ -518,10 +520,92 @@ void run_qkv_stage(const Lib &L, hipStream_t st, int T, int nq, int nk, int hd, 
   HIPCHECK(hipFree(stb));
 }
 
+// The Q/K step of a model without per-head norms, in place inside the fused
+// QKV row: RoPE only on Q and K, and with `bias` the QKV bias added to Q, K
+// and V first (src/asm/prefill_q8.inc:848-883 without the cache stores).
+void run_rope_only(const Lib &L, hipStream_t st, int T, int nq, int nk, int hd, bool bias, const Opts &opt) {
+  const long long ts = (long long)(nq + 2 * nk) * hd;
+  const int rw = nq + nk + (bias ? nk : 0);  // heads read and written per token
+  const double bytes = 2.0 * T * rw * hd * 4 + 2.0 * T * (hd / 2) * 4 + (bias ? (nq + 2.0 * nk) * hd * 4 : 0.0);
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(8);
+  std::vector<float *> qkv(sets);
+  for (int s = 0; s < sets; ++s) qkv[s] = device_fill<float>((size_t)T * ts, r, -1.f, 1.f);
+  float *b = bias ? device_fill<float>((size_t)ts, r, -0.5f, 0.5f) : nullptr;
+  float *ct = device_empty<float>((size_t)T * hd / 2), *stb = device_empty<float>((size_t)T * hd / 2);
+  if (L.build_rope_tables(ct, stb, T, hd, 1e6f)) {
+    printf("Fail: rope tables\n");
+    exit(1);
+  }
+  int iters = 0;
+  const double us = time_calls(L, st, sets, opt, [&](int s) {
+    v7g_qkv_stage g;
+    memset(&g, 0, sizeof(g));
+    g.q = {qkv[s], ts, nq, nullptr, b, nullptr, 0, 1};
+    g.k = {qkv[s] + (size_t)nq * hd, ts, nk, nullptr, b ? b + (size_t)nq * hd : nullptr, nullptr, 0, 1};
+    if (bias) g.v = {qkv[s] + (size_t)(nq + nk) * hd, ts, nk, nullptr, b + (size_t)(nq + nk) * hd, nullptr, 0, 1};
+    g.n_tokens = T;
+    g.head_dim = hd;
+    g.cos_table = ct;
+    g.sin_table = stb;
+    g.rope_max_dim = hd / 2;
+    g.table_rows = T;
+    g.eps = 1e-6f;
+    L.qkv_rope_stage(&g);
+  }, &iters);
+  char shape[128];
+  snprintf(shape, sizeof shape, "tokens=%d q_heads=%d kv_heads=%d head_dim=%d (RoPE only%s)", T, nq, nk, hd,
+           bias ? ", QKV bias" : "");
+  report("qkv_rope_stage", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) HIPCHECK(hipFree(qkv[s]));
+  if (b) HIPCHECK(hipFree(b));
+  HIPCHECK(hipFree(ct));
+  HIPCHECK(hipFree(stb));
+}
+
+// Open-weight model shapes (widths within the dim % 64, hidden % 64 and head_dim % 32 in [64, 512] contract of
+// tools/db_build_tool.c:2283-2300) for the `models` mode.
+struct ModelShape {
+  const char *name;
+  int dim, nq, nkv, hd, hidden, vocab;
+  bool qk_norm, qkv_bias;
+};
+
+const ModelShape kModels[] = {
+    {"TinyLlama-1.1B", 2048, 32, 4, 64, 5632, 32000, false, false},
+    {"Qwen3-4B", 2560, 32, 8, 128, 9728, 151936, true, false},
+    {"Phi-3-mini", 3072, 32, 32, 96, 8192, 32064, false, false},
+    {"Qwen2.5-7B", 3584, 28, 4, 128, 18944, 152064, false, true},
+    {"Gemma-3-12B", 3840, 16, 8, 256, 15360, 262144, true, false},
+    {"Llama-3-8B", 4096, 32, 8, 128, 14336, 128256, false, false},
+    {"Qwen3-14B", 5120, 40, 8, 128, 17408, 151936, true, false},
+    {"Llama-3-70B", 8192, 64, 8, 128, 28672, 128256, false, false},
+};
+
+// The four per-layer kernels of each model in kModels over `tokens` tokens.
+void run_models(const Lib &L, hipStream_t st, int tokens, const char *only, const Opts &opt) {
+  for (const ModelShape &m : kModels) {
+    if (only && strcmp(only, m.name)) continue;
+    printf("== %s: dim %d, %d Q / %d KV heads of %d, hidden %d, vocab %d%s%s\n", m.name, m.dim, m.nq, m.nkv, m.hd,
+           m.hidden, m.vocab, m.qk_norm ? ", Q/K norm" : "", m.qkv_bias ? ", QKV bias" : "");
+    fflush(stdout);
+    run_embedding(L, st, tokens, m.vocab, m.dim, opt);
+    run_add_rmsnorm(L, st, tokens, m.dim, opt);
+    if (m.qk_norm)
+      run_rope(L, st, tokens, m.nq, m.nkv, m.hd, opt);
+    else
+      run_rope_only(L, st, tokens, m.nq, m.nkv, m.hd, m.qkv_bias, opt);
+    run_swiglu(L, st, tokens, m.hidden, 32, true, opt);
+  }
+}
+
 int usage() {
   printf("usage: v7g_loadtest <libv7g.so> fused_add_rmsnorm <rows> <dim> | rmsnorm_rope <tokens> <q_heads> "
          "<kv_heads> <head_dim> | swiglu <rows> <hidden> | swiglu_q8 <rows> <hidden> [gs] | embedding <tokens> "
-         "<vocab> <dim> | configs   [--iterations N] [--time secs] [--no-rotate] [--per-row]\n");
+         "<vocab> <dim> | rmsnorm_quantize|add_rmsnorm_quantize <rows> <dim> [gs] | kv_pack|kv_pack_kv <tokens> <kv_dim> "
+         "| qkv_stage <tokens> <q_heads> <kv_heads> <head_dim> | rope_only <tokens> <q_heads> <kv_heads> <head_dim> "
+         "[bias] | configs | next | models [tokens] [name]   [--iterations N] [--time secs] [--no-rotate] "
+         "[--per-row]\n");
   return 1;
 }
 
@@ -583,6 +667,10 @@ int main(int argc, char **argv) {
     run_kv_pack(L, st, num(1, 0), num(2, 0), true, opt);
   else if (k == "qkv_stage" && pos.size() >= 5)
     run_qkv_stage(L, st, num(1, 0), num(2, 0), num(3, 0), num(4, 0), opt);
+  else if (k == "rope_only" && pos.size() >= 5)
+    run_rope_only(L, st, num(1, 0), num(2, 0), num(3, 0), num(4, 0), num(5, 0) != 0, opt);
+  else if (k == "models" && num(1, 8192) > 0)
+    run_models(L, st, num(1, 8192), pos.size() >= 3 ? pos[2].c_str() : nullptr, opt);
   else if (k == "next") {
     // The widened rows at the Qwen3-8B T=8192 shape (dim 4096, 32 Q / 8 KV heads of 128).
     run_norm_q8(L, st, 8192, 4096, 64, false, opt);
