@@ -70,8 +70,12 @@ def test_arith_selfcheck_exhaustive(ops):
 
 # --------------------------------------------------------------------------- embedding gather (a9)
 
+# Widths below 8192 that are not multiples of 4096 take one block per row sized to the row; 4096, 8192 and wider
+# rows take 256-thread blocks of 4096 codes (9216: a partial last block).
 @pytest.mark.parametrize("vocab,dim,n", [(1000, 64, 7), (512, 128, 33), (3000, 1024, 100), (4096, 4096, 257),
-                                         (700, 1088, 19), (900, 3072, 41)])
+                                         (700, 1088, 19), (900, 3072, 41), (600, 2048, 29), (500, 2560, 23),
+                                         (400, 3584, 17), (300, 5120, 31), (200, 7168, 9), (300, 8192, 21),
+                                         (100, 9216, 13)])
 def test_embedding_gather_matches_oracle(ops, oracle, vocab, dim, n):
     tq, ts = C.q8_table(11, vocab, dim)
     ids = C.rng(12).integers(0, vocab, n).astype(np.int32)
@@ -80,12 +84,13 @@ def test_embedding_gather_matches_oracle(ops, oracle, vocab, dim, n):
     assert_bits(host(got), want, "embedding")
 
 
-def test_embedding_invalid_ids_give_zero_rows(ops, oracle):
-    tq, ts = C.q8_table(3, 64, 128)
+@pytest.mark.parametrize("dim", [128, 5120, 9216])
+def test_embedding_invalid_ids_give_zero_rows(ops, oracle, dim):
+    tq, ts = C.q8_table(3, 64, dim)
     ids = np.array([0, -1, 63, 64, 1 << 30, 5], np.int32)
     got = host(ops.embedding_gather_q8(dev(ids), dev(tq), dev(ts)))
     valid = np.array([0, 63, 5])
-    want = oracle.embedding_gather(valid, tq, ts, 128)
+    want = oracle.embedding_gather(valid, tq, ts, dim)
     assert_bits(got[[0, 2, 5]], want, "valid rows")
     assert not got[[1, 3, 4]].any()
 

@@ -15,8 +15,13 @@
 // caches for the layer that reads them next; inside the per-layer chain at
 // T = 8192 they took the gather from 31.0 to 27.7 us with the same chain total
 // as streaming stores (the lines drain while the next kernels run).  Rows of
-// any dim % 64 == 0 take ceil(dim/4096) blocks; a partial last block clamps
-// its loads and predicates its stores.
+// dim % 4096 == 0 take dim/4096 such blocks.  Any other row up to 8192 codes is
+// one block of ceil(dim/16) threads rounded up to whole waves, so that no
+// wave of the launch is left without codes (with 256-thread blocks a row of
+// 5120 codes took a second block of which three waves had nothing to do:
+// 51.7% of the HBM peak against 63.2% at [8192 ids, 5120]; 56.2% against 60.6%
+// at 2048).  Wider rows take ceil(dim/4096) blocks of 256 threads.  A thread
+// whose dwords run past the row clamps its loads and predicates its stores.
 #include "v7g_device.h"
 #include "v7g_internal.h"
 
@@ -24,14 +29,15 @@ namespace v7g {
 
 constexpr unsigned kEmbDwords = 4;  // dwords (4 codes each) per thread
 
-__global__ __launch_bounds__(256) void embedding_gather_q8_kernel(float *__restrict__ out,
+__global__ __launch_bounds__(512) void embedding_gather_q8_kernel(float *__restrict__ out,
                                                                   const int32_t *__restrict__ ids,
                                                                   unsigned blocks_per_row,
                                                                   const int8_t *__restrict__ table_q,
                                                                   const float *__restrict__ table_s, int dim,
                                                                   int vocab) {
+  const unsigned tb = blockDim.x;
   const unsigned t = blockIdx.x / blocks_per_row;
-  const unsigned w0 = (blockIdx.x - t * blocks_per_row) * (256u * kEmbDwords) + threadIdx.x;
+  const unsigned w0 = (blockIdx.x - t * blocks_per_row) * (tb * kEmbDwords) + threadIdx.x;
   const unsigned dw = (unsigned)dim >> 2;  // dwords per row
   const int id = ids ? ids[t] : (int)t;    // no id array: row t of the table
   float *dst = out + (size_t)t * dim;
@@ -39,7 +45,7 @@ __global__ __launch_bounds__(256) void embedding_gather_q8_kernel(float *__restr
     // An id outside the table cannot be read; its row is written as zeros.
 #pragma unroll
     for (unsigned j = 0; j < kEmbDwords; ++j) {
-      const unsigned w = w0 + 256u * j;
+      const unsigned w = w0 + tb * j;
       if (w < dw) *reinterpret_cast<float4 *>(dst + 4 * w) = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     return;
@@ -51,14 +57,14 @@ __global__ __launch_bounds__(256) void embedding_gather_q8_kernel(float *__restr
   float s[kEmbDwords];
 #pragma unroll
   for (unsigned j = 0; j < kEmbDwords; ++j) {
-    const unsigned w = w0 + 256u * j;
+    const unsigned w = w0 + tb * j;
     const unsigned wc = w < dw ? w : dw - 1;
     q[j] = ld_stream_u32(src + wc);
     s[j] = sc[wc >> 4];
   }
 #pragma unroll
   for (unsigned j = 0; j < kEmbDwords; ++j) {
-    const unsigned w = w0 + 256u * j;
+    const unsigned w = w0 + tb * j;
     const uint32_t u = q[j];
     const float4 v = make_float4((float)((int32_t)(u << 24) >> 24) * s[j], (float)((int32_t)(u << 16) >> 24) * s[j],
                                  (float)((int32_t)(u << 8) >> 24) * s[j], (float)((int32_t)u >> 24) * s[j]);
@@ -68,11 +74,15 @@ __global__ __launch_bounds__(256) void embedding_gather_q8_kernel(float *__restr
 
 void launch_embedding_gather(float *out, const int32_t *ids, int n_tokens, const int8_t *table_q,
                              const float *table_s, int dim, int vocab, hipStream_t stream) {
-  const unsigned per_block = 256u * kEmbDwords;
-  const unsigned bpr = ((unsigned)dim / 4u + per_block - 1u) / per_block;
-  const unsigned blocks = (unsigned)n_tokens * bpr;
-  enqueue(embedding_gather_q8_kernel, dim3(blocks), dim3(256), 0, stream, out, ids, bpr, table_q, table_s,
-                     dim, vocab);
+  const unsigned dw = (unsigned)dim / 4u;
+  unsigned tb = 256u, bpr = (dw + 256u * kEmbDwords - 1u) / (256u * kEmbDwords);
+  if (dim % 4096 != 0 && dim <= 8192) {
+    tb = (dw + kEmbDwords - 1u) / kEmbDwords;
+    tb = (tb + 63u) / 64u * 64u;  // whole waves, at most 512 threads
+    bpr = 1u;
+  }
+  enqueue(embedding_gather_q8_kernel, dim3((unsigned)n_tokens * bpr), dim3(tb), 0, stream, out, ids, bpr, table_q,
+          table_s, dim, vocab);
 }
 
 }  // namespace v7g
