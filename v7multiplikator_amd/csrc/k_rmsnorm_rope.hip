@@ -272,7 +272,15 @@ __device__ float kZeroRow[256] = {};  // never written; not const, so it stays i
 // compile-time blocks) through one xor-4 exchange per block, and loads the
 // cos/sin entries of its own elements (j = e in the first half, e - hd/2 in
 // the second).
-template <int K>
+// BW (some side has a bias, and no side has both a bias and a norm weight:
+// the QKV bias of a model without Q/K norms): a side's bias goes through the
+// weight registers, with the other loads.  Otherwise a bias is read after the
+// other loads, one load at a time, each waited for (the compiler's choice
+// within 64 VGPRs), which cost the 28 Q / 4 KV head stage of 128 with QKV
+// bias 5.5 points of the HBM peak before BW; without a bias that form of the
+// kernel measured about 1 us faster on the Q/K/V stage than one with the bias
+// code taken out.
+template <int K, bool BW>
 __global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rmsnorm_rope_wave_kernel(RopeArgs a) {
   static_assert(K >= 2 && K <= 8, "head_dim 64 to 256");
   constexpr bool ODD = K % 2 == 1;
@@ -299,7 +307,18 @@ __global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rms
   if (bad_pos) pos = 0;
   const bool rot = S.rotate && pos != 0;
   const size_t row = (size_t)pos * (size_t)a.rope_max_dim + 4 * m;
-  const float *wp = S.norm_weight ? S.norm_weight + 4 * m : kZeroRow + 4 * m;
+  // BW: a side's bias is read into the weight registers, through a
+  // wave-uniform base and a 32-bit lane offset, so that the loads address
+  // through a scalar base as the norm weight's do.
+  const float *wp;
+  bool bias_in_w = false;
+  if constexpr (BW) {
+    bias_in_w = S.bias != nullptr;
+    const float *wbase = S.norm_weight ? S.norm_weight : (bias_in_w ? S.bias : kZeroRow);
+    wp = wbase + (bias_in_w ? (unsigned)in_head : 4u * m);
+  } else {
+    wp = S.norm_weight ? S.norm_weight + 4 * m : kZeroRow + 4 * m;
+  }
   const float *cp = rot ? a.cos_table + row : kZeroRow + 4 * m;
   const float *sp = rot ? a.sin_table + row : kZeroRow + 4 * m;
   // odd K: whether the lane's block k lies in the first half of the head
@@ -318,7 +337,13 @@ __global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rms
   // The loads above are issued here, ahead of the branches below (the
   // compiler would otherwise sink the weight and table loads past them).
   asm volatile("" ::: "memory");
-  if (S.bias) {
+  if constexpr (BW) {
+    if (bias_in_w) {
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        xv[k] = make_float4(xv[k].x + wv[k].x, xv[k].y + wv[k].y, xv[k].z + wv[k].z, xv[k].w + wv[k].w);
+    }
+  } else if (S.bias) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const float4 b = *reinterpret_cast<const float4 *>(S.bias + in_head + 32 * k);
@@ -390,7 +415,16 @@ static void launch_k(const RopeArgs &a, hipStream_t stream) {
   if constexpr (K <= 8) {
     // 64 threads per wave index in 32 bits: n_waves < 2^26 (the general kernel covers the rest)
     if (a.n_waves < (1u << 26)) {
-      enqueue((rmsnorm_rope_wave_kernel<K>), dim3((a.n_waves + 3u) / 4u), dim3(256), 0, stream, a);
+      bool any_bias = false, norm_and_bias = false;
+      for (int i = 0; i < a.n_sides; ++i) {
+        any_bias = any_bias || a.side[i].bias;
+        norm_and_bias = norm_and_bias || (a.side[i].bias && a.side[i].norm_weight);
+      }
+      const dim3 grid((a.n_waves + 3u) / 4u);
+      if (any_bias && !norm_and_bias)
+        enqueue((rmsnorm_rope_wave_kernel<K, true>), grid, dim3(256), 0, stream, a);
+      else
+        enqueue((rmsnorm_rope_wave_kernel<K, false>), grid, dim3(256), 0, stream, a);
       return;
     }
   }
