@@ -501,7 +501,8 @@ def test_rmsnorm_model_widths(ops, oracle, dim):
 
 
 @pytest.mark.parametrize("gs", [64, 32])
-@pytest.mark.parametrize("dim", [64, 128, 512, 544, 1024, 2048, 2560, 3072, 4096, 5120, 8192, 12288, 16384])
+@pytest.mark.parametrize("dim", [64, 128, 512, 544, 1024, 2048, 2560, 3072, 3584, 3840, 4096, 5120, 6144, 7168, 8192,
+                                 12288, 16384])
 def test_rmsnorm_quantize_rows(ops, oracle, gs, dim):
     if dim % gs:
         pytest.skip("dim must be a multiple of the group size")
@@ -515,7 +516,7 @@ def test_rmsnorm_quantize_rows(ops, oracle, gs, dim):
 
 
 @pytest.mark.parametrize("gs", [64, 32])
-@pytest.mark.parametrize("dim", [64, 2048, 2560, 4096, 12288])
+@pytest.mark.parametrize("dim", [64, 2048, 2560, 3072, 3584, 3840, 4096, 5120, 6144, 8192, 12288])
 def test_add_rmsnorm_quantize_equals_the_two_calls(ops, oracle, gs, dim):
     """The fused decode step equals v7s_add_inplace then v7s_rmsnorm_quantize (src/asm/forward_q8.inc:386-387)."""
     rows = 9

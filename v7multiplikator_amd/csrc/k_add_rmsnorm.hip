@@ -24,6 +24,8 @@
 //     normalised row quantized per group of 64 exactly as v7d_quantize does;
 //   and the Q8 decode step v7s_add_inplace -> v7s_rmsnorm_quantize
 //     (src/asm/forward_q8.inc:386-387), fused here into one pass.
+#include <type_traits>
+
 #include "v7g_device.h"
 #include "v7g_internal.h"
 
@@ -525,23 +527,26 @@ void launch_rmsnorm_quantize(int8_t *q, float *q_s, float *x, const float *add, 
     const unsigned lds = (unsigned)(dim + dim / 4) * sizeof(float);
     auto go = [&](auto kernel) { enqueue(kernel, grid, block, lds, stream, q, q_s, x, add, weight, dim, eps); };
     const bool g32 = gs == 32;
+    auto go_tpb = [&](auto tpb) {
+      constexpr int TPB = decltype(tpb)::value;
+      if (add)
+        go(g32 ? norm_q8_row16_kernel<TPB, 32, true> : norm_q8_row16_kernel<TPB, 64, true>);
+      else
+        go(g32 ? norm_q8_row16_kernel<TPB, 32, false> : norm_q8_row16_kernel<TPB, 64, false>);
+    };
+    // The block size compiled in for the common model widths: 0.2 to 2.7 points
+    // of the HBM peak above the run-time block size at [8192, dim].
     switch (dim) {
-      case 2048:
-        if (add) go(g32 ? norm_q8_row16_kernel<128, 32, true> : norm_q8_row16_kernel<128, 64, true>);
-        else go(g32 ? norm_q8_row16_kernel<128, 32, false> : norm_q8_row16_kernel<128, 64, false>);
-        break;
-      case 4096:
-        if (add) go(g32 ? norm_q8_row16_kernel<256, 32, true> : norm_q8_row16_kernel<256, 64, true>);
-        else go(g32 ? norm_q8_row16_kernel<256, 32, false> : norm_q8_row16_kernel<256, 64, false>);
-        break;
-      case 8192:
-        if (add) go(g32 ? norm_q8_row16_kernel<512, 32, true> : norm_q8_row16_kernel<512, 64, true>);
-        else go(g32 ? norm_q8_row16_kernel<512, 32, false> : norm_q8_row16_kernel<512, 64, false>);
-        break;
-      default:
-        if (add) go(g32 ? norm_q8_row16_kernel<0, 32, true> : norm_q8_row16_kernel<0, 64, true>);
-        else go(g32 ? norm_q8_row16_kernel<0, 32, false> : norm_q8_row16_kernel<0, 64, false>);
-        break;
+      case 2048: go_tpb(std::integral_constant<int, 128>{}); break;
+      case 2560: go_tpb(std::integral_constant<int, 160>{}); break;
+      case 3072: go_tpb(std::integral_constant<int, 192>{}); break;
+      case 3584: go_tpb(std::integral_constant<int, 224>{}); break;
+      case 3840: go_tpb(std::integral_constant<int, 240>{}); break;
+      case 4096: go_tpb(std::integral_constant<int, 256>{}); break;
+      case 5120: go_tpb(std::integral_constant<int, 320>{}); break;
+      case 6144: go_tpb(std::integral_constant<int, 384>{}); break;
+      case 8192: go_tpb(std::integral_constant<int, 512>{}); break;
+      default: go_tpb(std::integral_constant<int, 0>{}); break;
     }
     return;
   }
