@@ -233,10 +233,11 @@ def test_qk_rmsnorm_rope_config2(ops, oracle):
     assert_bits(out[:, (Hq + Hk) * D:], qkv[:, (Hq + Hk) * D:], "v untouched")
 
 
-@pytest.mark.parametrize("Hq,Hk,D", [(28, 4, 128), (14, 2, 64), (12, 2, 64)])
+@pytest.mark.parametrize("Hq,Hk,D", [(28, 4, 128), (14, 2, 64), (12, 2, 64), (16, 8, 256), (10, 3, 256), (5, 1, 256)])
 def test_qk_rmsnorm_rope_partial_waves(ops, oracle, Hq, Hk, D):
-    """Head counts that are not multiples of 8 (Qwen2.5-style 28 + 4, 14 + 2, 12 + 2): the wave kernel's
-    last wave of each side holds fewer than 8 heads; its spare lanes must store nothing."""
+    """Head counts that are not multiples of a wave's heads (Qwen2.5-style 28 + 4, 14 + 2, 12 + 2 at 8 heads per
+    wave; 10 + 3 and 5 + 1 at head_dim 256, 4 heads per wave of 16 lanes each): the last wave of each side holds
+    fewer heads; its spare lanes must store nothing."""
     T = 37
     qkv = C.normal(Hq * 100 + Hk, (T, (Hq + 2 * Hk) * D))
     qw, kw = C.norm_weight(Hq + 1, D), C.norm_weight(Hk + 2, D)

@@ -40,7 +40,7 @@ struct RopeArgs {
   int n_heads0, n_heads01;  // side 0 heads; sides 0 + 1 heads
   int heads_per_token;      // heads of all sides
   unsigned n_heads;         // n_tokens * heads_per_token
-  // The wave kernel's grid: per token, ceil(heads / 8) waves for each side.
+  // The wave kernels' grid: per token, ceil(heads / 8) waves for each side (heads / 4 at head_dim 256).
   int wave0, wave01;        // side 0 waves; sides 0 + 1 waves
   int waves_per_token;
   unsigned n_waves;         // n_tokens * waves_per_token
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_lds_kernel(RopeArgs a) {
 // most float 4*7 + 32*7 + 3.
 __device__ float kZeroRow[256] = {};  // never written; not const, so it stays in the global address space
 
-// head_dim 64 to 256: each wave takes up to 8 heads of one side of one token
+// head_dim 64 to 224: each wave takes up to 8 heads of one side of one token
 // (ceil(heads / 8) waves per side and token), so the side, its descriptor
 // fields and the position are read once per wave with scalar loads, instead
 // of per lane from the kernel arguments with vector loads, whose in-order
@@ -262,7 +262,7 @@ __device__ float kZeroRow[256] = {};  // never written; not const, so it stays i
 // weights or rotation reads kZeroRow instead).  Lanes past the side's last
 // head repeat that head's loads, which the same instructions fetch anyway, and
 // store nothing.  The arithmetic is rmsnorm_rope_reg_kernel's.  At most 64
-// VGPRs (8 waves per SIMD) up to head_dim 128; 104-127 from 160 to 256, where
+// VGPRs (8 waves per SIMD) up to head_dim 128; 86-127 from 160 to 224, where
 // having every load in flight still beats the per-lane kernels' occupancy.
 //
 // head_dim % 64 == 32 (odd K): the rotate-half partner of lane m's block k is
@@ -282,7 +282,7 @@ __device__ float kZeroRow[256] = {};  // never written; not const, so it stays i
 // code taken out.
 template <int K, bool BW>
 __global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rmsnorm_rope_wave_kernel(RopeArgs a) {
-  static_assert(K >= 2 && K <= 8, "head_dim 64 to 256");
+  static_assert(K >= 2 && K <= 7, "head_dim 64 to 224 (256: rmsnorm_rope_wave16_kernel)");
   constexpr bool ODD = K % 2 == 1;
   constexpr int KH = K / 2;         // even K: the partner of block k is block k + KH in the same lane
   constexpr int KC = ODD ? K : KH;  // cos/sin float4 per lane
@@ -410,6 +410,140 @@ __global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rms
   }
 }
 
+// head_dim 256 in 16 lanes per head (4 heads per wave): in the 8-lane layout
+// a lane holds 8 float4 of the head and 8 of the weights (110 VGPRs, 4 waves
+// per SIMD).  Here the two 8-lane halves take alternate 32-element blocks:
+// lane (h, m) holds x[64k + 32h + 4m .. +3], k < 4, i.e. blocks 2k + h.  The
+// 32 FMA chains still run in the reference's order, block 0 to 7: after
+// block b the accumulators live in half b & 1, and one DPP rotation by 8
+// within the 16-lane row hands them to the other half for block b + 1.  The
+// (A+B)+(C+D) + HADD_YMM exchanges (lanes m ^ 2, ^ 4, ^ 1) run inside each
+// half; half 1 holds the result and rotates the scale back to half 0.  The
+// rotate-half partner of block b is block b + 4, the same half, two
+// registers on (k + 2), so the rotation stays in registers; the cos/sin
+// entries of a lane's first-half elements are j = 64k + 32h + 4m .. +3, k < 2.
+// Same side mapping, loads and stores as rmsnorm_rope_wave_kernel.
+__device__ __forceinline__ float ror8_f(float v) {  // lane l gets lane l ^ 8 of its 16-lane row
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+}
+
+template <bool BW>
+__global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave16_kernel(RopeArgs a) {
+  constexpr int HD = 256;
+  const int m = threadIdx.x & 7;
+  const int h = (threadIdx.x >> 3) & 1;
+  const unsigned lane_off = 32u * h + 4u * m;  // the lane's first element of its head
+  const unsigned wi = __builtin_amdgcn_readfirstlane((blockIdx.x * 256u + threadIdx.x) >> 6);  // wave index
+  const bool live_wave = wi < a.n_waves;
+  const unsigned wvv = live_wave ? wi : 0u;
+  const unsigned t = wvv / (unsigned)a.waves_per_token;
+  const int r = (int)(wvv - t * (unsigned)a.waves_per_token);
+  const int sd = r < a.wave0 ? 0 : (r < a.wave01 ? 1 : 2);
+  const RopeSide &S = a.side[sd];
+  const int hs_raw = 4 * (r - (sd == 0 ? 0 : (sd == 1 ? a.wave0 : a.wave01))) + ((threadIdx.x & 63) >> 4);
+  const bool live = live_wave && hs_raw < S.n_heads;
+  const int hs = hs_raw < S.n_heads ? hs_raw : S.n_heads - 1;
+  const size_t in_head = (size_t)hs * HD + lane_off;
+  float *x = S.buf + (size_t)t * (size_t)S.token_stride + in_head;
+  int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
+  // A position outside the tables cannot be read: its rotated heads become NaN.
+  const bool bad_pos = S.rotate && pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
+  if (bad_pos) pos = 0;
+  const bool rot = S.rotate && pos != 0;
+  const size_t row = (size_t)pos * (size_t)a.rope_max_dim + lane_off;
+  const float *wp;
+  bool bias_in_w = false;
+  if constexpr (BW) {
+    bias_in_w = S.bias != nullptr;
+    const float *wbase = S.norm_weight ? S.norm_weight : (bias_in_w ? S.bias : kZeroRow);
+    wp = wbase + (bias_in_w ? (unsigned)in_head : lane_off);
+  } else {
+    wp = S.norm_weight ? S.norm_weight + lane_off : kZeroRow + lane_off;
+  }
+  // kZeroRow covers floats up to lane_off + 64*3 + 3 <= 255
+  const float *cp = rot ? a.cos_table + row : kZeroRow + lane_off;
+  const float *sp = rot ? a.sin_table + row : kZeroRow + lane_off;
+  float4 xv[4], wv[4], c[2], sn[2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) xv[k] = ld_stream4(x + 64 * k);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) wv[k] = *reinterpret_cast<const float4 *>(wp + 64 * k);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    c[k] = *reinterpret_cast<const float4 *>(cp + 64 * k);
+    sn[k] = *reinterpret_cast<const float4 *>(sp + 64 * k);
+  }
+  asm volatile("" ::: "memory");
+  if constexpr (BW) {
+    if (bias_in_w) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        xv[k] = make_float4(xv[k].x + wv[k].x, xv[k].y + wv[k].y, xv[k].z + wv[k].z, xv[k].w + wv[k].w);
+    }
+  } else if (S.bias) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 b = *reinterpret_cast<const float4 *>(S.bias + in_head + 64 * k);
+      xv[k] = make_float4(xv[k].x + b.x, xv[k].y + b.y, xv[k].z + b.z, xv[k].w + b.w);
+    }
+  }
+  float4 xn[4];
+  if (S.norm_weight) {  // uniform over the wave: every lane takes part in the rotations
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      if (b > 0) acc = make_float4(ror8_f(acc.x), ror8_f(acc.y), ror8_f(acc.z), ror8_f(acc.w));
+      const float4 v = xv[b >> 1];  // block b in half b & 1 (the other half's result is not used)
+      acc = make_float4(__builtin_fmaf(v.x, v.x, acc.x), __builtin_fmaf(v.y, v.y, acc.y),
+                        __builtin_fmaf(v.z, v.z, acc.z), __builtin_fmaf(v.w, v.w, acc.w));
+    }
+    acc.x = acc.x + xor_f(acc.x, 2); acc.y = acc.y + xor_f(acc.y, 2);
+    acc.z = acc.z + xor_f(acc.z, 2); acc.w = acc.w + xor_f(acc.w, 2);
+    acc.x = acc.x + xor_f(acc.x, 4); acc.y = acc.y + xor_f(acc.y, 4);
+    acc.z = acc.z + xor_f(acc.z, 4); acc.w = acc.w + xor_f(acc.w, 4);
+    acc.x = acc.x + xor_f(acc.x, 1); acc.y = acc.y + xor_f(acc.y, 1);
+    acc.z = acc.z + xor_f(acc.z, 1); acc.w = acc.w + xor_f(acc.w, 1);
+    const float t0 = acc.x + acc.y;
+    const float t2 = acc.z + acc.w;
+    const float s1 = rms_scale(t0 + t2, (float)HD, a.eps);  // valid in half 1
+    const float s0 = ror8_f(s1);
+    const float s = h ? s1 : s0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      xn[k] = make_float4((xv[k].x * s) * wv[k].x, (xv[k].y * s) * wv[k].y, (xv[k].z * s) * wv[k].z,
+                          (xv[k].w * s) * wv[k].w);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xn[k] = xv[k];
+  }
+  if (bad_pos) {
+    const float q = __builtin_nanf("");
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xn[k] = make_float4(q, q, q, q);
+  }
+  if (rot) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float4 ev = xn[k], od = xn[k + 2];
+      xn[k] = make_float4(__builtin_fmaf(-od.x, sn[k].x, ev.x * c[k].x), __builtin_fmaf(-od.y, sn[k].y, ev.y * c[k].y),
+                          __builtin_fmaf(-od.z, sn[k].z, ev.z * c[k].z), __builtin_fmaf(-od.w, sn[k].w, ev.w * c[k].w));
+      xn[k + 2] = make_float4(__builtin_fmaf(od.x, c[k].x, ev.x * sn[k].x), __builtin_fmaf(od.y, c[k].y, ev.y * sn[k].y),
+                              __builtin_fmaf(od.z, c[k].z, ev.z * sn[k].z), __builtin_fmaf(od.w, c[k].w, ev.w * sn[k].w));
+    }
+  }
+  if (live) {
+    if (!S.cache || S.keep_f32) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) st_stream4(x + 64 * k, xn[k]);
+    }
+    if (S.cache) {
+      uint16_t *kc = S.cache + (size_t)t * (size_t)S.cache_stride + in_head;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) st_stream_u2(reinterpret_cast<uint32_t *>(kc + 64 * k), pack4_f16(xn[k]));
+    }
+  }
+}
+
 template <int K>
 static void launch_k(const RopeArgs &a, hipStream_t stream) {
   if constexpr (K <= 8) {
@@ -420,11 +554,18 @@ static void launch_k(const RopeArgs &a, hipStream_t stream) {
         any_bias = any_bias || a.side[i].bias;
         norm_and_bias = norm_and_bias || (a.side[i].bias && a.side[i].norm_weight);
       }
+      const bool bw = any_bias && !norm_and_bias;
       const dim3 grid((a.n_waves + 3u) / 4u);
-      if (any_bias && !norm_and_bias)
+      if constexpr (K == 8) {  // head_dim 256: 4 heads per wave (the host's wave layout)
+        if (bw)
+          enqueue((rmsnorm_rope_wave16_kernel<true>), grid, dim3(256), 0, stream, a);
+        else
+          enqueue((rmsnorm_rope_wave16_kernel<false>), grid, dim3(256), 0, stream, a);
+      } else if (bw) {
         enqueue((rmsnorm_rope_wave_kernel<K, true>), grid, dim3(256), 0, stream, a);
-      else
+      } else {
         enqueue((rmsnorm_rope_wave_kernel<K, false>), grid, dim3(256), 0, stream, a);
+      }
       return;
     }
   }
@@ -447,7 +588,9 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.n_heads01 = a.n_heads0 + (n_sides > 1 ? sides[1].n_heads : 0);
   a.heads_per_token = a.n_heads01 + (n_sides > 2 ? sides[2].n_heads : 0);
   a.n_heads = (unsigned)n_tokens * (unsigned)a.heads_per_token;
-  auto waves = [&](int i) { return i < n_sides ? (sides[i].n_heads + 7) / 8 : 0; };
+  // heads per wave: 8 (8 lanes per head), 4 at head_dim 256 (16 lanes per head)
+  const int hpw = head_dim == 256 ? 4 : 8;
+  auto waves = [&](int i) { return i < n_sides ? (sides[i].n_heads + hpw - 1) / hpw : 0; };
   a.wave0 = waves(0);
   a.wave01 = a.wave0 + waves(1);
   a.waves_per_token = a.wave01 + waves(2);
