@@ -233,11 +233,12 @@ def test_qk_rmsnorm_rope_config2(ops, oracle):
     assert_bits(out[:, (Hq + Hk) * D:], qkv[:, (Hq + Hk) * D:], "v untouched")
 
 
-@pytest.mark.parametrize("Hq,Hk,D", [(28, 4, 128), (14, 2, 64), (12, 2, 64), (16, 8, 256), (10, 3, 256), (5, 1, 256)])
+@pytest.mark.parametrize("Hq,Hk,D", [(28, 4, 128), (14, 2, 64), (12, 2, 64), (20, 6, 64), (32, 17, 64), (40, 8, 96),
+                                     (17, 1, 96), (16, 8, 256), (10, 3, 256), (5, 1, 256)])
 def test_qk_rmsnorm_rope_partial_waves(ops, oracle, Hq, Hk, D):
-    """Head counts that are not multiples of a wave's heads (Qwen2.5-style 28 + 4, 14 + 2, 12 + 2 at 8 heads per
-    wave; 10 + 3 and 5 + 1 at head_dim 256, 4 heads per wave of 16 lanes each): the last wave of each side holds
-    fewer heads; its spare lanes must store nothing."""
+    """Head counts that are not multiples of a wave's heads (Qwen2.5-style 28 + 4, and 14 + 2 up to 40 + 8 at
+    head_dim 64 and 96, at 8 heads per wave; 10 + 3 and 5 + 1 at head_dim 256, 4 heads per wave of 16 lanes each):
+    the last wave of each side holds fewer heads; its spare lanes must store nothing."""
     T = 37
     qkv = C.normal(Hq * 100 + Hk, (T, (Hq + 2 * Hk) * D))
     qw, kw = C.norm_weight(Hq + 1, D), C.norm_weight(Hk + 2, D)
