@@ -628,6 +628,30 @@ int main(int argc, char **argv) {
       pos.push_back(argv[i]);
   }
   if (pos.empty() || opt.iterations < 1) return usage();
+  // The mode and its positional arguments are checked before the library or the GPU is touched.
+  static const struct {
+    const char *mode;
+    size_t min_args;  // positional arguments including the mode
+  } kModes[] = {{"fused_add_rmsnorm", 3}, {"rmsnorm_rope", 5}, {"swiglu", 3}, {"swiglu_q8", 3}, {"embedding", 4},
+                {"rmsnorm_quantize", 3}, {"add_rmsnorm_quantize", 3}, {"kv_pack", 3}, {"kv_pack_kv", 3},
+                {"qkv_stage", 5}, {"rope_only", 5}, {"models", 1}, {"next", 1}, {"configs", 1}};
+  bool known = false;
+  for (const auto &md : kModes) known = known || (pos[0] == md.mode && pos.size() >= md.min_args);
+  if (!known) return usage();
+  for (size_t i = 1; i < pos.size(); ++i) {
+    const bool model_name = pos[0] == "models" && i == 2;
+    if (!model_name && atoi(pos[i].c_str()) <= 0 && !(pos[0] == "rope_only" && i == 5)) return usage();
+  }
+  if (pos[0] == "models" && pos.size() >= 3) {
+    bool found = false;
+    for (const ModelShape &m : kModels) found = found || pos[2] == m.name;
+    if (!found) {
+      printf("Fail: no model shape named %s; the shapes:", pos[2].c_str());
+      for (const ModelShape &m : kModels) printf(" %s", m.name);
+      printf("\n");
+      return 1;
+    }
+  }
   Lib L;
   if (load(argv[1], L)) return 1;
   if (L.init()) {
