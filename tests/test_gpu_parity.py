@@ -195,10 +195,11 @@ def test_rmsnorm_rope_validator_cases(ops, oracle, heads, hd, pos, eps, seed):
 @pytest.mark.parametrize("H", [3, 8])
 @pytest.mark.parametrize("hd", [64, 96, 128, 160, 192, 224, 256, 288, 480, 512])
 def test_rmsnorm_rope_head_dims(ops, oracle, hd, H):
-    """Every head_dim % 32 == 0 in [64, 512] class: the wave kernel up to 256 (the rotate-half partner in the
-    same lane, or for hd % 64 == 32 in lane m ^ 4), the per-lane kernels above (register rotation for
-    hd % 64 == 0, LDS rotation otherwise).  37 tokens x 3 or 8 heads: partly filled waves, and with 8 heads
-    the last workgroup's last three waves hold no head."""
+    """Every head_dim % 32 == 0 in [64, 512] class: the wave kernel up to 224 (the rotate-half partner in the
+    same lane, or for hd % 64 == 32 in lane m ^ 4), 16 lanes per head at 256 (the FMA chains handed between the
+    two halves), the per-lane kernels above (register rotation for hd % 64 == 0, LDS rotation otherwise).
+    37 tokens x 3 or 8 heads: partly filled waves, and with 8 heads the last workgroup's last waves hold no
+    head."""
     T = 37
     buf = C.normal(hd, (T, H, hd))
     w = C.norm_weight(hd + 1, hd)
