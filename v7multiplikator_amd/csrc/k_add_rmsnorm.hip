@@ -472,9 +472,10 @@ static auto fixed_row_kernel() {
 // 1024 < dim <= 8192, dim % 256 == 0 (dim = 4 * threads * chunks): the shape
 // that measured fastest at [8192, dim] for the common model widths, compiled
 // in (2560, 3072, 3584, 3840, 5120, 8192: 1.5 to 2.5 points of the HBM peak
-// above the general kernel, 8192 even); a run-time thread count with 2, 1 or
-// 4 chunks per thread for the other multiples of 256 up to 4096 and of 512 up
-// to 8192 (whole waves, at most 1024 threads).  2048 and 4096 keep the
+// above the general kernel, 8192 even); a run-time thread count with 2
+// chunks per thread (1 where dim/4 is an odd multiple of 64) for the other
+// multiples of 256 up to 4096 and of 512 up to 8192 (whole waves, at most
+// 1024 threads).  2048 and 4096 keep the
 // dispatch_rows shapes, which measured best.  Returns false where none applies.
 template <bool ADD>
 static bool launch_fixed_row(const RowLaunch &L, float *o, float *x, const float *add, const float *weight,
@@ -499,8 +500,6 @@ static bool launch_fixed_row(const RowLaunch &L, float *o, float *x, const float
     go(fixed_row_kernel<ADD, 0, 2>(), chunks / 2);
   else if (chunks <= 1024)
     go(fixed_row_kernel<ADD, 0, 1>(), chunks);
-  else if (chunks % 256 == 0)
-    go(fixed_row_kernel<ADD, 0, 4>(), chunks / 4);
   else
     return false;
   return true;
