@@ -4,9 +4,12 @@ The fixed-shape tests pin the benchmark configurations and the reference validat
 sweep draws the shape parameters at random inside each entry's contract (rows, row lengths that are
 not multiples of the vector width, ragged quantization tails, every head_dim class, tables wider than
 head_dim / 2, positions anywhere in the table) so that an indexing mistake that only shows at an
-unusual shape fails here.  Each case names its parameters in the failure message.
+unusual shape fails here.  Each case names its parameters in the failure message.  V7G_SWEEP_CASES
+(default 12) and V7G_SWEEP_SEED (default 0) widen or move the sweep, e.g. for a longer run by hand.
 """
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -17,7 +20,8 @@ pytestmark = pytest.mark.gpu
 
 torch = pytest.importorskip("torch")
 
-CASES = 12
+CASES = int(os.environ.get("V7G_SWEEP_CASES", "12"))
+SEED = int(os.environ.get("V7G_SWEEP_SEED", "0"))
 
 
 @pytest.fixture(scope="module")
@@ -50,7 +54,7 @@ def same(a, b):
 
 def shapes(tag, draw):
     """CASES parameter sets from a generator seeded by the test's tag."""
-    r = np.random.default_rng(sum(map(ord, tag)) * 7919)
+    r = np.random.default_rng(sum(map(ord, tag)) * 7919 + SEED)
     return [draw(r) for _ in range(CASES)]
 
 
