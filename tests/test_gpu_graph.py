@@ -1,9 +1,10 @@
-"""The batched entries under HIP graph capture: the per-layer chain (Q8 embedding gather, add+RMSNorm,
+"""The batched entries and the drop-ins under HIP graph capture: the per-layer chain (Q8 embedding gather, add+RMSNorm,
 Q/K RMSNorm+RoPE inside a fused QKV row, SwiGLU -> Q8) and the RMSNorm -> Q8 / K/V pack rows, captured once
 with torch.cuda.graph on torch's capture stream (the library binds to the caller's current stream) and
 replayed several times, with eager work between the replays (the in-place inputs restored, the outputs
-cleared), each replay checked bit for bit against one eager pass of the same calls.  None of these entries
-records a memset or allocates inside the capture.
+cleared), each replay checked bit for bit against one eager pass of the same calls; and a one-token decode
+step of reference-signature drop-in calls, captured the same way.  None of these entries records a memset or
+allocates inside the capture.
 """
 from __future__ import annotations
 
@@ -123,3 +124,106 @@ def test_chain_replays_from_a_hip_graph(ops, oracle):
         # the library binds each host thread to the stream of its last call: back to the current stream
         from v7multiplikator_amd import _lib
         _lib.load().v7g_set_stream(torch.cuda.current_stream().cuda_stream)
+
+
+def test_dropin_decode_step_replays_from_a_hip_graph(ops, oracle):
+    """A one-token decode step made of the reference-signature drop-ins (ms_abi, through tests/libdropin_shim.so,
+    as a v7 host calls them): the embedding row, add+RMSNorm, Q and K RMSNorm+RoPE at position 37, the K row
+    packed to binary16, SwiGLU -> Q8 of the FFN row.  Captured once on torch's capture stream (bound with
+    v7g_set_stream inside the capture), replayed four times with eager work between, each replay equal to one
+    eager pass bit for bit: one graph launch instead of six kernel launches."""
+    import ctypes
+    import os
+
+    from v7multiplikator_amd import _lib
+    shim_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdropin_shim.so")
+    if not os.path.exists(shim_path):
+        pytest.fail(f"{shim_path} is missing: run __graft_entry__.build()")
+    S = ctypes.CDLL(shim_path)
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    S.shim_embedding_row.argtypes = [vp, i, i, vp, vp]
+    S.shim_fused_add_rmsnorm.argtypes = [vp, vp, vp, vp, i]
+    S.shim_rmsnorm_rope_heads.argtypes = [vp, i, i, vp, vp, vp, i, i]
+    S.shim_kv_pack_f16.argtypes = [vp, vp, i]
+    S.shim_swiglu_quantize_row.argtypes = [vp, vp, vp, vp, i]
+    L = _lib.load()
+    L.v7g_set_rms_eps(ctypes.c_float(1e-6))
+    POS = 37
+    tq, ts = C.q8_table(31, VOCAB, DIM)
+    tq, ts = dev(tq), dev(ts)
+    residual0 = dev(C.normal(32, DIM))
+    w = dev(C.norm_weight(33, DIM))
+    qkv0 = dev(C.normal(34, (NQ + 2 * NKV) * HD))
+    qw, kw = dev(C.norm_weight(35, HD)), dev(C.norm_weight(36, HD))
+    ct, st = oracle.rope_tables(64, HD, 1e6)
+    ct, st = dev(ct), dev(st)
+    gate, up = dev(C.normal(37, HID, 1.5)), dev(C.normal(38, HID, 1.5))
+
+    emb = torch.empty(DIM, device="cuda")
+    residual = residual0.clone()
+    normed = torch.empty(DIM, device="cuda")
+    qkv = qkv0.clone()
+    kc = torch.empty(NKV * HD, dtype=torch.float16, device="cuda")
+    codes = torch.empty(HID, dtype=torch.int8, device="cuda")
+    scales = torch.empty(HID // 64, device="cuda")
+    p = lambda t: t.data_ptr()  # noqa: E731
+
+    def step():
+        L.v7g_set_stream(torch.cuda.current_stream().cuda_stream)
+        S.shim_embedding_row(p(emb), 123, DIM, p(tq), p(ts))
+        S.shim_fused_add_rmsnorm(p(normed), p(residual), p(emb), p(w), DIM)
+        S.shim_rmsnorm_rope_heads(p(qkv), NQ, HD, p(qw), p(ct), p(st), POS, HD // 2)
+        S.shim_rmsnorm_rope_heads(p(qkv) + NQ * HD * 4, NKV, HD, p(kw), p(ct), p(st), POS, HD // 2)
+        S.shim_kv_pack_f16(p(kc), p(qkv) + NQ * HD * 4, NKV * HD)
+        S.shim_swiglu_quantize_row(p(codes), p(gate), p(up), p(scales), HID)
+
+    outs = (emb, residual, normed, qkv, kc, codes, scales)
+
+    def reset():
+        residual.copy_(residual0)
+        qkv.copy_(qkv0)
+        for o in (emb, normed, scales):
+            o.fill_(-1.0)
+        codes.fill_(0)
+        kc.fill_(0)
+
+    L.v7g_clear_last_error()
+    reset()
+    step()
+    torch.cuda.synchronize()
+    assert L.v7g_get_last_error() == 0
+    want = [bits(o) for o in outs]
+    # the eager pass against the oracle: the decode step's results are the reference's
+    r_new = C.normal(32, DIM) + oracle.embedding_gather(np.array([123], np.int32), host_np(tq), host_np(ts), DIM)[0]
+    assert np.array_equal(want[1], r_new.astype(np.float32).view(np.uint32))
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        reset()
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+
+    g = torch.cuda.CUDAGraph()
+    reset()
+    torch.cuda.synchronize()
+    try:
+        with torch.cuda.graph(g):
+            step()
+        torch.cuda.synchronize()
+        for replay in range(4):
+            reset()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            for o, w_, name in zip(outs, want, ("emb", "residual", "normed", "qkv", "k cache", "codes", "scales")):
+                assert np.array_equal(bits(o), w_), (replay, name)
+        assert L.v7g_get_last_error() == 0
+    finally:
+        L.v7g_set_stream(torch.cuda.current_stream().cuda_stream)
+        L.v7g_clear_last_error()
+
+
+def host_np(t):
+    return t.detach().cpu().numpy()
