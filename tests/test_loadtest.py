@@ -16,7 +16,8 @@ EXE = os.path.join(PKG, "v7g_loadtest")
 LIB = os.path.join(PKG, "libv7g.so")
 
 MODES = ["fused_add_rmsnorm", "rmsnorm_rope", "swiglu", "swiglu_q8", "embedding", "rmsnorm_quantize",
-         "add_rmsnorm_quantize", "kv_pack", "kv_pack_kv", "qkv_stage", "rope_only", "configs", "next", "models"]
+         "add_rmsnorm_quantize", "kv_pack", "kv_pack_kv", "qkv_stage", "rope_only", "configs", "next", "models",
+         "decode"]
 
 
 @pytest.fixture(scope="module")
@@ -87,3 +88,13 @@ def test_single_kernel_modes(exe, args, kernel):
     recs = records(r.stdout)
     assert len(recs) == 1 and recs[0]["kernel"] == kernel, recs
     assert recs[0]["us"] > 0 and "cache-resident" in r.stdout
+
+
+@pytest.mark.gpu
+def test_decode_mode_times_eager_and_graph_steps(exe):
+    r = run(exe, LIB, "decode", 4, "--iterations", 5)
+    assert r.returncode == 0, r.stdout + r.stderr
+    recs = records(r.stdout)
+    assert len(recs) == 1 and recs[0]["kernel"] == "decode_step" and recs[0]["tokens"] == 4, recs
+    for key in ("eager_us", "host_us_per_call", "graph_per_step_us", "graph_all_steps_us"):
+        assert recs[0][key] > 0, key

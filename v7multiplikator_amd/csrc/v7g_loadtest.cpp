@@ -18,6 +18,7 @@
 //   v7g_loadtest <libv7g.so> configs          (every benchmark configuration below)
 //   v7g_loadtest <libv7g.so> next             (the widened rows at the Qwen3-8B T=8192 shape)
 //   v7g_loadtest <libv7g.so> models [tokens] [name]  (the per-layer kernels at other model shapes)
+//   v7g_loadtest <libv7g.so> decode [tokens]  (small-batch steps: eager launches against HIP graphs)
 //   options: --iterations N  --time secs  --no-rotate  --per-row
 //
 // Like the reference harnesses it loads the library with dlopen and resolves
@@ -40,6 +41,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <chrono>
 #include <thread>
 #include <vector>
 
@@ -78,6 +80,9 @@ struct Lib {
   int (*kv_pack_f16_kv)(uint16_t *, long long, uint16_t *, long long, const float *, const float *, long long, int,
                         int);
   int (*qkv_rope_stage)(const v7g_qkv_stage *);
+  int (*qk_rmsnorm_rope_kv)(float *, long long, int, const float *, float *, long long, int, const float *, int, int,
+                            const float *, const float *, const int32_t *, int, int, int, float, uint16_t *, long long,
+                            int);
   v7s_fused_add_rmsnorm_fn v7s_fused_add_rmsnorm;
   v7s_rmsnorm_rope_heads_fn v7s_rmsnorm_rope_heads;
   v7s_swiglu_quantize_row_fn v7s_swiglu_quantize_row;
@@ -117,6 +122,7 @@ int load(const char *path, Lib &L) {
   resolve(L, L.kv_pack_f16, "v7g_kv_pack_f16");
   resolve(L, L.kv_pack_f16_kv, "v7g_kv_pack_f16_kv");
   resolve(L, L.qkv_rope_stage, "v7g_qkv_rope_stage");
+  resolve(L, L.qk_rmsnorm_rope_kv, "v7g_qk_rmsnorm_rope_kv");
   resolve(L, L.v7s_fused_add_rmsnorm, "v7s_fused_add_rmsnorm");
   resolve(L, L.v7s_rmsnorm_rope_heads, "v7s_rmsnorm_rope_heads");
   resolve(L, L.v7s_swiglu_quantize_row, "v7s_swiglu_quantize_row");
@@ -599,13 +605,109 @@ void run_models(const Lib &L, hipStream_t st, int tokens, const char *only, cons
   }
 }
 
+// Small-batch (decode) steps at the Qwen3-8B shape: per step the embedding gather, add+RMSNorm, Q/K
+// RMSNorm+RoPE with the K cache rows, the V cache rows and SwiGLU -> Q8 for `tokens` tokens.  Eager launches
+// (host time per call and step time), one HIP graph per step replayed, and one graph of all the steps.
+void run_decode(const Lib &L, hipStream_t st, int T, const Opts &opt) {
+  const int DIM = 4096, VOCAB = 151936, NQ = 32, NKV = 8, HD = 128, HID = 12288, GS = 32, POS = 4096;
+  const int N = opt.iterations;
+  const long long qs = (long long)(NQ + 2 * NKV) * HD;
+  Rng r(9);
+  int8_t *tq = device_empty<int8_t>((size_t)VOCAB * DIM);
+  HIPCHECK(hipMemset(tq, 1, (size_t)VOCAB * DIM));
+  float *ts = device_fill<float>((size_t)VOCAB * DIM / 64, r, 0.001f, 0.02f);
+  float *out = device_empty<float>((size_t)T * DIM), *normed = device_empty<float>((size_t)T * DIM);
+  float *res = device_fill<float>((size_t)T * DIM, r, -1.f, 1.f), *w = device_fill<float>(DIM, r, 0.5f, 1.5f);
+  float *qkv = device_fill<float>((size_t)T * qs, r, -1.f, 1.f);
+  float *qw = device_fill<float>(HD, r, 0.5f, 1.5f), *kw = device_fill<float>(HD, r, 0.5f, 1.5f);
+  float *gate = device_fill<float>((size_t)T * HID, r, -3.f, 3.f), *up = device_fill<float>((size_t)T * HID, r, -3.f, 3.f);
+  int8_t *codes = device_empty<int8_t>((size_t)T * HID);
+  float *scales = device_empty<float>((size_t)T * HID / GS);
+  uint16_t *kc = device_empty<uint16_t>((size_t)T * NKV * HD), *vc = device_empty<uint16_t>((size_t)T * NKV * HD);
+  float *ct = device_empty<float>((size_t)POS * HD / 2), *stb = device_empty<float>((size_t)POS * HD / 2);
+  if (L.build_rope_tables(ct, stb, POS, HD, 1e6f)) {
+    printf("Fail: rope tables\n");
+    exit(1);
+  }
+  std::vector<int32_t> hv(T);
+  for (int i = 0; i < T; ++i) hv[i] = (int32_t)(((uint64_t)i * 7919u) % VOCAB);
+  int32_t *ids = device_empty<int32_t>(T), *pos = device_empty<int32_t>(T);
+  HIPCHECK(hipMemcpy(ids, hv.data(), T * 4, hipMemcpyHostToDevice));
+  for (int i = 0; i < T; ++i) hv[i] = (1000 + i) % POS;
+  HIPCHECK(hipMemcpy(pos, hv.data(), T * 4, hipMemcpyHostToDevice));
+  int bad = 0;
+  auto step = [&]() {
+    bad |= L.embedding_gather_q8(out, ids, T, tq, ts, DIM, VOCAB);
+    bad |= L.fused_add_rmsnorm(normed, res, out, w, T, DIM, 1e-6f);
+    bad |= L.qk_rmsnorm_rope_kv(qkv, qs, NQ, qw, qkv + NQ * HD, qs, NKV, kw, T, HD, ct, stb, pos, 0, HD / 2, POS, 1e-6f,
+                                kc, NKV * HD, 0);
+    bad |= L.kv_pack_f16(vc, NKV * HD, qkv + (NQ + NKV) * HD, qs, T, NKV * HD);
+    bad |= L.swiglu_q8(codes, scales, gate, up, T, HID, GS);
+  };
+  constexpr int kCalls = 5;
+  hipEvent_t e0, e1;
+  HIPCHECK(hipEventCreate(&e0));
+  HIPCHECK(hipEventCreate(&e1));
+  auto gpu_us = [&](auto run) {
+    run();
+    HIPCHECK(hipStreamSynchronize(st));
+    HIPCHECK(hipEventRecord(e0, st));
+    run();
+    HIPCHECK(hipEventRecord(e1, st));
+    HIPCHECK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIPCHECK(hipEventElapsedTime(&ms, e0, e1));
+    return ms * 1e3 / N;
+  };
+  const double eager = gpu_us([&]() { for (int i = 0; i < N; ++i) step(); });
+  HIPCHECK(hipStreamSynchronize(st));
+  const auto h0 = std::chrono::steady_clock::now();
+  for (int i = 0; i < N; ++i) step();
+  const auto h1 = std::chrono::steady_clock::now();
+  HIPCHECK(hipStreamSynchronize(st));
+  const double host_call = std::chrono::duration<double, std::micro>(h1 - h0).count() / (N * kCalls);
+  hipGraph_t g1, gn;
+  hipGraphExec_t x1, xn;
+  HIPCHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  step();
+  HIPCHECK(hipStreamEndCapture(st, &g1));
+  HIPCHECK(hipGraphInstantiate(&x1, g1, nullptr, nullptr, 0));
+  HIPCHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  for (int i = 0; i < N; ++i) step();
+  HIPCHECK(hipStreamEndCapture(st, &gn));
+  HIPCHECK(hipGraphInstantiate(&xn, gn, nullptr, nullptr, 0));
+  const double g_each = gpu_us([&]() { for (int i = 0; i < N; ++i) HIPCHECK(hipGraphLaunch(x1, st)); });
+  const double g_all = gpu_us([&]() { HIPCHECK(hipGraphLaunch(xn, st)); });
+  if (bad || L.get_last_error()) {
+    printf("Fail: a call failed (%d)\n", bad);
+    exit(1);
+  }
+  printf("Pass: decode step, tokens=%d (5 calls) iterations=%d\n", T, N);
+  printf("  eager %.2f us / step (host %.2f us / call), graph per step %.2f us, graph of %d steps %.2f us / step\n",
+         eager, host_call, g_each, N, g_all);
+  printf("{\"kernel\": \"decode_step\", \"tokens\": %d, \"eager_us\": %.3f, \"host_us_per_call\": %.3f, "
+         "\"graph_per_step_us\": %.3f, \"graph_all_steps_us\": %.3f, \"steps\": %d}\n",
+         T, eager, host_call, g_each, g_all, N);
+  fflush(stdout);
+  HIPCHECK(hipGraphExecDestroy(x1));
+  HIPCHECK(hipGraphExecDestroy(xn));
+  HIPCHECK(hipGraphDestroy(g1));
+  HIPCHECK(hipGraphDestroy(gn));
+  HIPCHECK(hipEventDestroy(e0));
+  HIPCHECK(hipEventDestroy(e1));
+  for (void *p : {(void *)tq, (void *)ts, (void *)out, (void *)normed, (void *)res, (void *)w, (void *)qkv, (void *)qw,
+                  (void *)kw, (void *)gate, (void *)up, (void *)codes, (void *)scales, (void *)kc, (void *)vc,
+                  (void *)ct, (void *)stb, (void *)ids, (void *)pos})
+    HIPCHECK(hipFree(p));
+}
+
 int usage() {
   printf("usage: v7g_loadtest <libv7g.so> fused_add_rmsnorm <rows> <dim> | rmsnorm_rope <tokens> <q_heads> "
          "<kv_heads> <head_dim> | swiglu <rows> <hidden> | swiglu_q8 <rows> <hidden> [gs] | embedding <tokens> "
          "<vocab> <dim> | rmsnorm_quantize|add_rmsnorm_quantize <rows> <dim> [gs] | kv_pack|kv_pack_kv <tokens> <kv_dim> "
          "| qkv_stage <tokens> <q_heads> <kv_heads> <head_dim> | rope_only <tokens> <q_heads> <kv_heads> <head_dim> "
-         "[bias] | configs | next | models [tokens] [name]   [--iterations N] [--time secs] [--no-rotate] "
-         "[--per-row]\n");
+         "[bias] | configs | next | models [tokens] [name] | decode [tokens]   [--iterations N] [--time secs] "
+         "[--no-rotate] [--per-row]\n");
   return 1;
 }
 
@@ -634,7 +736,7 @@ int main(int argc, char **argv) {
     size_t min_args;  // positional arguments including the mode
   } kModes[] = {{"fused_add_rmsnorm", 3}, {"rmsnorm_rope", 5}, {"swiglu", 3}, {"swiglu_q8", 3}, {"embedding", 4},
                 {"rmsnorm_quantize", 3}, {"add_rmsnorm_quantize", 3}, {"kv_pack", 3}, {"kv_pack_kv", 3},
-                {"qkv_stage", 5}, {"rope_only", 5}, {"models", 1}, {"next", 1}, {"configs", 1}};
+                {"qkv_stage", 5}, {"rope_only", 5}, {"models", 1}, {"next", 1}, {"configs", 1}, {"decode", 1}};
   bool known = false;
   for (const auto &md : kModes) known = known || (pos[0] == md.mode && pos.size() >= md.min_args);
   if (!known) return usage();
@@ -693,7 +795,12 @@ int main(int argc, char **argv) {
     run_qkv_stage(L, st, num(1, 0), num(2, 0), num(3, 0), num(4, 0), opt);
   else if (k == "rope_only" && pos.size() >= 5)
     run_rope_only(L, st, num(1, 0), num(2, 0), num(3, 0), num(4, 0), num(5, 0) != 0, opt);
-  else if (k == "models" && num(1, 8192) > 0)
+  else if (k == "decode") {
+    if (pos.size() >= 2)
+      run_decode(L, st, num(1, 1), opt);
+    else
+      for (int T : {1, 8, 32, 64, 256}) run_decode(L, st, T, opt);
+  } else if (k == "models" && num(1, 8192) > 0)
     run_models(L, st, num(1, 8192), pos.size() >= 3 ? pos[2].c_str() : nullptr, opt);
   else if (k == "next") {
     // The widened rows at the Qwen3-8B T=8192 shape (dim 4096, 32 Q / 8 KV heads of 128).
