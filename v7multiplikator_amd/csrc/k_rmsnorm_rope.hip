@@ -24,8 +24,10 @@
 // runs in the reference order; the xor exchanges 2, 4, 1 are exactly the
 // (A+B)+(C+D) and HADD_YMM pairings.  When head_dim % 64 == 0 the rotate-half
 // partner of block k is block k + K/2 in the same lane, so the rotation
-// happens in registers; otherwise the normalised head goes through LDS to
-// meet its partner.  Heads are read and written in place with streaming
+// happens in registers; otherwise it is in lane m ^ 4 (the wave kernel's
+// lane exchange) or goes through LDS (the per-lane kernel).  At head_dim 256
+// a head spans 16 lanes, the two halves holding alternate blocks, and the
+// chains pass from one half to the other after each block (same order).  Heads are read and written in place with streaming
 // loads and stores (the norm weights and the cos/sin rows, shared by every
 // head of a token, stay cached).  The result is bit-identical to the
 // reference.
