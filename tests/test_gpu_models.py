@@ -1,11 +1,12 @@
 """The four per-layer kernels at the model shapes of the load test's `models` mode (csrc/v7g_loadtest.cpp
-kModels: the published widths, head counts, head_dims, QKV bias / Q-K norm and intermediate sizes of eight
-open-weight models), bit for bit against the oracle on a few tokens: the Q8 embedding gather (a small vocabulary
-at the model's width), add+RMSNorm over the width, the Q/K step inside the fused QKV row (RMSNorm+RoPE with Q/K
-norms, else RoPE only with the QKV bias added to Q, K and V first where the model has one, and the K/V binary16
-cache rows), and SwiGLU -> Q8 over the intermediate size (32-element groups).  Every shape-specific launch the
-library picks for these shapes (the fixed-length add+RMSNorm rows, embedding blocks sized to the row, the bias
-through the weight registers, 16 lanes per head at head_dim 256) runs here."""
+kModels: the published widths, head counts, head_dims, QKV bias / Q-K norm and intermediate sizes of twelve
+open-weight models), bit for bit against the oracle: the Q8 embedding gather (a small vocabulary at the model's
+width), add+RMSNorm over the width, the Q/K step inside the fused QKV row (RMSNorm+RoPE with Q/K norms, else RoPE
+only with the QKV bias added to Q, K and V first where the model has one, and the K/V binary16 cache rows), and
+SwiGLU -> Q8 over the intermediate size (32-element groups).  11 tokens, 2053 for the Q/K step.  Every
+shape-specific launch the library picks for these shapes (the fixed-length add+RMSNorm rows, embedding blocks sized
+to the row, the bias through the weight registers, 16 lanes per head at head_dim 256, the flat layout for head
+counts that are not multiples of 8) runs here."""
 from __future__ import annotations
 
 import numpy as np
@@ -19,7 +20,11 @@ torch = pytest.importorskip("torch")
 
 # name, dim, q heads, kv heads, head_dim, hidden, Q/K norm, QKV bias (the load test's model table)
 MODELS = [
+    ("Qwen2.5-0.5B", 896, 14, 2, 64, 4864, False, True),
+    ("Llama-3.2-1B", 2048, 32, 8, 64, 8192, False, False),
     ("TinyLlama-1.1B", 2048, 32, 4, 64, 5632, False, False),
+    ("Qwen2.5-1.5B", 1536, 12, 2, 128, 8960, False, True),
+    ("Gemma-2-2B", 2304, 8, 4, 256, 9216, False, False),
     ("Qwen3-4B", 2560, 32, 8, 128, 9728, True, False),
     ("Phi-3-mini", 3072, 32, 32, 96, 8192, False, False),
     ("Qwen2.5-7B", 3584, 28, 4, 128, 18944, False, True),
@@ -28,7 +33,8 @@ MODELS = [
     ("Qwen3-14B", 5120, 40, 8, 128, 17408, True, False),
     ("Llama-3-70B", 8192, 64, 8, 128, 28672, False, False),
 ]
-T = 11
+T_ROWS = 11
+T_QKV = 2053  # the Q/K/V stage over more than 2048 tokens: head counts that are not multiples of 8 take the flat layout
 
 
 @pytest.fixture(scope="module")
@@ -59,6 +65,7 @@ def same(a, b):
 @pytest.mark.parametrize("name,dim,nq,nkv,hd,hidden,qk_norm,bias", MODELS, ids=[m[0] for m in MODELS])
 def test_model_layer_kernels(ops, oracle, name, dim, nq, nkv, hd, hidden, qk_norm, bias):
     seed = dim + hd
+    T = T_ROWS
     # Q8 embedding gather at the model's width (a 300-row table; the kernel's blocks depend on the width only)
     tq, ts = C.q8_table(seed, 300, dim)
     ids = C.rng(seed).integers(0, 300, T).astype(np.int32)
@@ -73,6 +80,7 @@ def test_model_layer_kernels(ops, oracle, name, dim, nq, nkv, hd, hidden, qk_nor
     assert same(host(rt), want_r) and same(host(got_o), want_o), "add+RMSNorm"
 
     # the Q/K step inside the fused QKV row, with the K/V cache rows
+    T = T_QKV
     qkv = C.normal(seed + 4, (T, (nq + 2 * nkv) * hd))
     qw, kw = C.norm_weight(seed + 5, hd), C.norm_weight(seed + 6, hd)
     qb = C.normal(seed + 7, nq * hd, 0.5) if bias else None
@@ -80,7 +88,7 @@ def test_model_layer_kernels(ops, oracle, name, dim, nq, nkv, hd, hidden, qk_nor
     vb = C.normal(seed + 9, nkv * hd, 0.5) if bias else None
     ct, st = oracle.rope_tables(T + 4, hd, 1e6)
     pos = (np.arange(T) + 3).astype(np.int32)
-    pos[2] = 0
+    pos[[2, 1000]] = 0
     q_np = qkv[:, :nq * hd].reshape(T, nq, hd)
     k_np = qkv[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd)
     v_np = qkv[:, (nq + nkv) * hd:].reshape(T, nkv, hd)
@@ -112,6 +120,7 @@ def test_model_layer_kernels(ops, oracle, name, dim, nq, nkv, hd, hidden, qk_nor
                     oracle.rmsnorm_rope(k_np, kw, ct, st, pos, 1e-6)), "k"
 
     # SwiGLU -> Q8 over the intermediate size
+    T = T_ROWS
     g, u = C.normal(seed + 10, (T, hidden), 1.5), C.normal(seed + 11, (T, hidden), 1.5)
     want_q, want_s = oracle.swiglu_q8(g, u, 32)
     got_q, got_s = ops.swiglu_q8(dev(g), dev(u), gs=32)

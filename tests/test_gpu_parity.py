@@ -258,6 +258,69 @@ def test_qk_rmsnorm_rope_partial_waves(ops, oracle, Hq, Hk, D):
     assert_bits(out[:, (Hq + Hk) * D:], qkv[:, (Hq + Hk) * D:], "v untouched")
 
 
+@pytest.mark.parametrize("T,nq,nkv,hd,norm,bias,keep_k,keep_v,pos0", [
+    (2049, 14, 2, 64, False, True, True, True, None),     # Qwen2.5-0.5B: bias through the weight registers
+    (1024, 12, 2, 128, False, True, False, True, None),   # Qwen2.5-1.5B at 1024 tokens (half the lanes would idle)
+    (2048, 28, 4, 128, True, True, True, False, None),    # norm weight and bias on one side
+    (2055, 7, 1, 96, True, False, True, True, 5),         # odd head_dim / 32, positions pos0 + t
+    (2050, 3, 3, 160, False, False, True, True, None),
+    (2051, 12, 4, 192, False, True, True, True, None),
+    (2053, 5, 2, 224, True, True, False, False, None)])
+def test_qkv_stage_flat_layout(ops, oracle, T, nq, nkv, hd, norm, bias, keep_k, keep_v, pos0):
+    """From 1024 or 2048 tokens, head counts that are not multiples of 8 below head_dim 256 take the flat layout
+    (8 (token, head) pairs of one side per wave, tokens in groups of 8, each lane group with its own position):
+    last groups of fewer than 8 tokens, positions 0 (no rotation) and past the tables (NaN in Q and K, V kept),
+    every head_dim / 32 from 2 to 7, bias or norm weight or both, cache rows with and without the f32 result."""
+    s = T + 7 * nq + hd
+    qkv = C.normal(s, (T, (nq + 2 * nkv) * hd))
+    qw, kw = C.norm_weight(s + 1, hd), C.norm_weight(s + 2, hd)
+    qb = C.normal(s + 3, nq * hd, 0.5) if bias else None
+    kb = C.normal(s + 4, nkv * hd, 0.5) if bias else None
+    vb = C.normal(s + 5, nkv * hd, 0.5) if bias else None
+    n_pos = 3000
+    ct, st = oracle.rope_tables(n_pos, hd, 1e6 if hd % 64 == 0 else 1e4)
+    bad = np.array([], np.int64)
+    if pos0 is None:
+        pos = C.rng(s + 6).integers(0, n_pos, T).astype(np.int32)
+        pos[[0, 9, T - 1]] = 0
+        bad = np.array([3, 17, T - 2])
+        pos[bad] = [n_pos, n_pos + 100, 2 ** 31 - 1]
+    else:
+        pos = (np.arange(T) + pos0).astype(np.int32)
+    q_np = qkv[:, :nq * hd].reshape(T, nq, hd)
+    k_np = qkv[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd)
+    v_np = qkv[:, (nq + nkv) * hd:].reshape(T, nkv, hd)
+    opos = pos.copy()
+    opos[bad] = 0  # the oracle's tables have no such rows; these tokens are checked for NaN below
+    wq, wk, wv, wkc, wvc = oracle.qkv_stage(q_np, k_np, v_np, qw if norm else None, kw if norm else None, qb, kb, vb,
+                                            ct, st, opos, 1e-6)
+    t = dev(qkv)
+    q = t[:, :nq * hd].view(T, nq, hd)
+    k = t[:, nq * hd:(nq + nkv) * hd].view(T, nkv, hd)
+    v = t[:, (nq + nkv) * hd:].view(T, nkv, hd)
+    kc = torch.zeros((T, nkv, hd), dtype=torch.float16, device="cuda")
+    vc = torch.zeros((T, nkv, hd), dtype=torch.float16, device="cuda")
+    d = lambda a: None if a is None else dev(a)  # noqa: E731
+    ops.qkv_rope_stage(q, k, v, dev(ct), dev(st), positions=None if pos0 is not None else dev(pos),
+                       pos0=pos0 or 0, eps=1e-6, q_norm_weight=d(qw) if norm else None,
+                       k_norm_weight=d(kw) if norm else None, q_bias=d(qb), k_bias=d(kb), v_bias=d(vb), k_cache=kc,
+                       v_cache=vc, keep_k_f32=keep_k, keep_v_f32=keep_v)
+    out = host(t)
+    gq = out[:, :nq * hd].reshape(T, nq, hd)
+    gk = out[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd)
+    gv = out[:, (nq + nkv) * hd:].reshape(T, nkv, hd)
+    gkc, gvc = host(kc), host(vc)
+    ok = np.setdiff1d(np.arange(T), bad)
+    assert_bits(gq[ok], wq[ok], "q")
+    assert_bits(gk[ok], (wk if keep_k else k_np)[ok], "k")
+    assert_bits(gv, wv if keep_v else v_np, "v")
+    assert_bits(gkc.view(np.uint16)[ok], wkc[ok], "k cache")
+    assert_bits(gvc.view(np.uint16), wvc, "v cache")
+    assert np.isnan(gq[bad]).all() and np.isnan(gkc[bad].astype(np.float32)).all()
+    if keep_k:
+        assert np.isnan(gk[bad]).all()
+
+
 @pytest.mark.parametrize("H", [2, 8])
 def test_rope_position_outside_tables_gives_nan(ops, oracle, H):
     buf = C.normal(9, (3, H, 64))

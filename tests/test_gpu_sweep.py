@@ -177,37 +177,53 @@ def test_sweep_qkv_stage(ops, oracle):
         return (int(r.integers(1, 24)), int(r.integers(1, 20)), int(r.integers(1, 9)), 32 * int(r.integers(2, 9)),
                 bool(r.integers(0, 2)), bool(r.integers(0, 2)), bool(r.integers(0, 2)), bool(r.integers(0, 2)))
 
-    for T, nq, nkv, hd, norm, bias, keep_k, keep_v in shapes("qkv", draw):
-        case = (T, nq, nkv, hd, norm, bias, keep_k, keep_v)
-        s = T * 31 + nq * 7 + nkv + hd
-        qkv = C.normal(s, (T, (nq + 2 * nkv) * hd))
-        qw, kw = C.norm_weight(s + 1, hd), C.norm_weight(s + 2, hd)
-        qb = C.normal(s + 3, nq * hd, 0.5) if bias else None
-        kb = C.normal(s + 4, nkv * hd, 0.5) if bias else None
-        vb = C.normal(s + 5, nkv * hd, 0.5) if bias else None
-        n_pos = T + 5
-        ct, st = oracle.rope_tables(n_pos, hd, 1e6 if hd % 64 == 0 else 1e4)
-        pos = C.rng(s + 6).integers(0, n_pos, T).astype(np.int32)
-        pos[0] = 0
-        q_np = qkv[:, :nq * hd].reshape(T, nq, hd)
-        k_np = qkv[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd)
-        v_np = qkv[:, (nq + nkv) * hd:].reshape(T, nkv, hd)
-        wq, wk, wv, wkc, wvc = oracle.qkv_stage(q_np, k_np, v_np, qw if norm else None, kw if norm else None,
-                                                qb, kb, vb, ct, st, pos, 1e-6)
-        t = dev(qkv)
-        q = t[:, :nq * hd].view(T, nq, hd)
-        k = t[:, nq * hd:(nq + nkv) * hd].view(T, nkv, hd)
-        v = t[:, (nq + nkv) * hd:].view(T, nkv, hd)
-        kc = torch.zeros((T, nkv, hd), dtype=torch.float16, device="cuda")
-        vc = torch.zeros((T, nkv, hd), dtype=torch.float16, device="cuda")
-        d = lambda a: None if a is None else dev(a)  # noqa: E731
-        ops.qkv_rope_stage(q, k, v, dev(ct), dev(st), positions=dev(pos), eps=1e-6,
-                           q_norm_weight=d(qw) if norm else None, k_norm_weight=d(kw) if norm else None,
-                           q_bias=d(qb), k_bias=d(kb), v_bias=d(vb), k_cache=kc, v_cache=vc, keep_k_f32=keep_k,
-                           keep_v_f32=keep_v)
-        out = host(t)
-        assert same(out[:, :nq * hd].reshape(T, nq, hd), wq), ("q",) + case
-        assert same(out[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd), wk if keep_k else k_np), ("k",) + case
-        assert same(out[:, (nq + nkv) * hd:].reshape(T, nkv, hd), wv if keep_v else v_np), ("v",) + case
-        assert same(host(kc).view(np.uint16), wkc), ("k cache",) + case
-        assert same(host(vc).view(np.uint16), wvc), ("v cache",) + case
+    for case in shapes("qkv", draw):
+        qkv_case(ops, oracle, *case)
+
+
+def test_sweep_qkv_stage_large(ops, oracle):
+    """The same over 1024 to 2600 tokens (a quarter of the cases), where head counts that are not multiples of 8
+    take the flat layout (8 (token, head) pairs of one side per wave, tokens in groups of 8)."""
+    def draw(r):
+        return (int(r.integers(1024, 2601)), int(r.integers(1, 20)), int(r.integers(1, 9)),
+                32 * int(r.integers(2, 9)), bool(r.integers(0, 2)), bool(r.integers(0, 2)), bool(r.integers(0, 2)),
+                bool(r.integers(0, 2)))
+
+    for case in shapes("qkv_large", draw)[:max(1, CASES // 4)]:
+        qkv_case(ops, oracle, *case)
+
+
+def qkv_case(ops, oracle, T, nq, nkv, hd, norm, bias, keep_k, keep_v):
+    case = (T, nq, nkv, hd, norm, bias, keep_k, keep_v)
+    s = T * 31 + nq * 7 + nkv + hd
+    qkv = C.normal(s, (T, (nq + 2 * nkv) * hd))
+    qw, kw = C.norm_weight(s + 1, hd), C.norm_weight(s + 2, hd)
+    qb = C.normal(s + 3, nq * hd, 0.5) if bias else None
+    kb = C.normal(s + 4, nkv * hd, 0.5) if bias else None
+    vb = C.normal(s + 5, nkv * hd, 0.5) if bias else None
+    n_pos = T + 5
+    ct, st = oracle.rope_tables(n_pos, hd, 1e6 if hd % 64 == 0 else 1e4)
+    pos = C.rng(s + 6).integers(0, n_pos, T).astype(np.int32)
+    pos[0] = 0
+    q_np = qkv[:, :nq * hd].reshape(T, nq, hd)
+    k_np = qkv[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd)
+    v_np = qkv[:, (nq + nkv) * hd:].reshape(T, nkv, hd)
+    wq, wk, wv, wkc, wvc = oracle.qkv_stage(q_np, k_np, v_np, qw if norm else None, kw if norm else None,
+                                            qb, kb, vb, ct, st, pos, 1e-6)
+    t = dev(qkv)
+    q = t[:, :nq * hd].view(T, nq, hd)
+    k = t[:, nq * hd:(nq + nkv) * hd].view(T, nkv, hd)
+    v = t[:, (nq + nkv) * hd:].view(T, nkv, hd)
+    kc = torch.zeros((T, nkv, hd), dtype=torch.float16, device="cuda")
+    vc = torch.zeros((T, nkv, hd), dtype=torch.float16, device="cuda")
+    d = lambda a: None if a is None else dev(a)  # noqa: E731
+    ops.qkv_rope_stage(q, k, v, dev(ct), dev(st), positions=dev(pos), eps=1e-6,
+                       q_norm_weight=d(qw) if norm else None, k_norm_weight=d(kw) if norm else None,
+                       q_bias=d(qb), k_bias=d(kb), v_bias=d(vb), k_cache=kc, v_cache=vc, keep_k_f32=keep_k,
+                       keep_v_f32=keep_v)
+    out = host(t)
+    assert same(out[:, :nq * hd].reshape(T, nq, hd), wq), ("q",) + case
+    assert same(out[:, nq * hd:(nq + nkv) * hd].reshape(T, nkv, hd), wk if keep_k else k_np), ("k",) + case
+    assert same(out[:, (nq + nkv) * hd:].reshape(T, nkv, hd), wv if keep_v else v_np), ("v",) + case
+    assert same(host(kc).view(np.uint16), wkc), ("k cache",) + case
+    assert same(host(vc).view(np.uint16), wvc), ("v cache",) + case

@@ -42,7 +42,8 @@ struct RopeArgs {
   int n_heads0, n_heads01;  // side 0 heads; sides 0 + 1 heads
   int heads_per_token;      // heads of all sides
   unsigned n_heads;         // n_tokens * heads_per_token
-  // The wave kernels' grid: per token, ceil(heads / 8) waves for each side (heads / 4 at head_dim 256).
+  // The wave kernels' grid: per token, ceil(heads / 8) waves for each side (heads / 4 at head_dim 256);
+  // the flat kernel's: per group of 8 tokens, heads waves for each side (waves_per_token then counts a group).
   int wave0, wave01;        // side 0 waves; sides 0 + 1 waves
   int waves_per_token;
   unsigned n_waves;         // n_tokens * waves_per_token
@@ -546,8 +547,171 @@ __global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave16_kernel(RopeArgs a)
   }
 }
 
+// Head counts that are not multiples of 8 (2 KV heads, 12, 14 or 28 Q heads),
+// from 1024 tokens: rmsnorm_rope_wave_kernel's last wave of such a side holds
+// only its leftover heads, and its idle lanes still issue every instruction (a
+// side of 2 heads fills a quarter of its wave).  Here tokens go in groups of 8 and each side's
+// (token, head) pairs of a group are dealt out 8 to a wave in token-major
+// order, so every wave is full: side s takes n_s waves per group, and lane
+// group g of wave j holds pair 8j + g, i.e. token 8*group + (8j + g) / n_s,
+// head (8j + g) % n_s.  The side's descriptor stays wave-uniform; the position
+// is per lane (its load goes out first, so the wait for it covers no other
+// load), and so are the table rows, the out-of-table NaN and the pos == 0
+// case, which keeps the unrotated head by a select (the rotation is computed
+// for every lane; a head's 8 lanes share one token).  Arithmetic, order and
+// bias handling (BW) are rmsnorm_rope_wave_kernel's.
+template <int K, bool BW>
+__global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rmsnorm_rope_flat_kernel(RopeArgs a) {
+  static_assert(K >= 2 && K <= 7, "head_dim 64 to 224");
+  constexpr bool ODD = K % 2 == 1;
+  constexpr int KH = K / 2;
+  constexpr int KC = ODD ? K : KH;
+  constexpr int J = (K - 1) / 2;
+  const int m = threadIdx.x & 7;
+  const bool lo = m < 4;
+  const unsigned wi = __builtin_amdgcn_readfirstlane((blockIdx.x * 256u + threadIdx.x) >> 6);  // wave index
+  const bool live_wave = wi < a.n_waves;
+  const unsigned wvv = live_wave ? wi : 0u;
+  const unsigned grp = wvv / (unsigned)a.waves_per_token;  // waves_per_token: waves per group of 8 tokens
+  const int r = (int)(wvv - grp * (unsigned)a.waves_per_token);
+  const int sd = r < a.wave0 ? 0 : (r < a.wave01 ? 1 : 2);
+  const RopeSide &S = a.side[sd];
+  const unsigned n_tokens = a.n_heads / (unsigned)a.heads_per_token;
+  const unsigned nh = (unsigned)S.n_heads;
+  const unsigned pair = 8u * (unsigned)(r - (sd == 0 ? 0 : (sd == 1 ? a.wave0 : a.wave01))) +
+                        ((threadIdx.x & 63u) >> 3);
+  const unsigned tl = pair / nh;
+  const int h = (int)(pair - tl * nh);
+  const unsigned t = 8u * grp + tl;
+  const bool live = live_wave && t < n_tokens;
+  const unsigned tt = t < n_tokens ? t : n_tokens - 1;
+  int pos = a.positions ? a.positions[tt] : a.pos0 + (int)tt;
+  asm volatile("" ::: "memory");  // the position's load goes out ahead of the head's
+  const size_t in_head = (size_t)h * a.head_dim + 4 * m;
+  float *x = S.buf + (size_t)tt * (size_t)S.token_stride + in_head;
+  const float *wp;
+  bool bias_in_w = false;
+  if constexpr (BW) {
+    bias_in_w = S.bias != nullptr;
+    const float *wbase = S.norm_weight ? S.norm_weight : (bias_in_w ? S.bias : kZeroRow);
+    wp = wbase + (bias_in_w ? (unsigned)in_head : 4u * m);
+  } else {
+    wp = S.norm_weight ? S.norm_weight + 4 * m : kZeroRow + 4 * m;
+  }
+  auto first_half = [&](int k) { return lo ? k <= J : k < J; };
+  float4 xv[K], wv[K], c[KC], sn[KC];
+#pragma unroll
+  for (int k = 0; k < K; ++k) xv[k] = ld_stream4(x + 32 * k);
+#pragma unroll
+  for (int k = 0; k < K; ++k) wv[k] = *reinterpret_cast<const float4 *>(wp + 32 * k);
+  asm volatile("" ::: "memory");
+  // A position outside the tables cannot be read: its rotated heads become NaN.
+  const bool bad_pos = S.rotate && pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
+  if (bad_pos) pos = 0;
+  const bool rot = S.rotate && pos != 0;
+  const size_t row = (size_t)pos * (size_t)a.rope_max_dim + 4 * m;
+  const float *cp = rot ? a.cos_table + row : kZeroRow + 4 * m;
+  const float *sp = rot ? a.sin_table + row : kZeroRow + 4 * m;
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int off = (!ODD || first_half(k)) ? 32 * k : 32 * k - 16 * K;
+    c[k] = *reinterpret_cast<const float4 *>(cp + off);
+    sn[k] = *reinterpret_cast<const float4 *>(sp + off);
+  }
+  asm volatile("" ::: "memory");
+  if constexpr (BW) {
+    if (bias_in_w) {
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        xv[k] = make_float4(xv[k].x + wv[k].x, xv[k].y + wv[k].y, xv[k].z + wv[k].z, xv[k].w + wv[k].w);
+    }
+  } else if (S.bias) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float4 b = *reinterpret_cast<const float4 *>(S.bias + in_head + 32 * k);
+      xv[k] = make_float4(xv[k].x + b.x, xv[k].y + b.y, xv[k].z + b.z, xv[k].w + b.w);
+    }
+  }
+  float4 xn[K];
+  if (S.norm_weight) {
+    const float sc = head_scale<K>(xv, 32 * K, a.eps);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      xn[k] = make_float4((xv[k].x * sc) * wv[k].x, (xv[k].y * sc) * wv[k].y, (xv[k].z * sc) * wv[k].z,
+                          (xv[k].w * sc) * wv[k].w);
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) xn[k] = xv[k];
+  }
+  if (bad_pos) {
+    const float q = __builtin_nanf("");
+#pragma unroll
+    for (int k = 0; k < K; ++k) xn[k] = make_float4(q, q, q, q);
+  }
+  float4 xr[K];  // the rotated head; kept only where rot holds
+  if constexpr (!ODD) {
+#pragma unroll
+    for (int k = 0; k < KH; ++k) {
+      const float4 ev = xn[k], od = xn[k + KH];
+      xr[k] = make_float4(__builtin_fmaf(-od.x, sn[k].x, ev.x * c[k].x), __builtin_fmaf(-od.y, sn[k].y, ev.y * c[k].y),
+                          __builtin_fmaf(-od.z, sn[k].z, ev.z * c[k].z), __builtin_fmaf(-od.w, sn[k].w, ev.w * c[k].w));
+      xr[k + KH] = make_float4(__builtin_fmaf(od.x, c[k].x, ev.x * sn[k].x), __builtin_fmaf(od.y, c[k].y, ev.y * sn[k].y),
+                               __builtin_fmaf(od.z, c[k].z, ev.z * sn[k].z), __builtin_fmaf(od.w, c[k].w, ev.w * sn[k].w));
+    }
+  } else {  // every lane takes part in the exchanges (a head's 8 lanes share its token, hence rot)
+    float4 part[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int kp_for_lo = k <= J ? k + J : k - J - 1;      // partner in lanes 0..3
+      const int kp_for_hi = k <= J - 1 ? k + J + 1 : k - J;  // partner in lanes 4..7
+      const float4 snd = lo ? xn[kp_for_hi] : xn[kp_for_lo];
+      part[k] = make_float4(xor_f(snd.x, 4), xor_f(snd.y, 4), xor_f(snd.z, 4), xor_f(snd.w, 4));
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float4 me = xn[k], pa = part[k];
+      if (first_half(k))
+        xr[k] = make_float4(__builtin_fmaf(-pa.x, sn[k].x, me.x * c[k].x), __builtin_fmaf(-pa.y, sn[k].y, me.y * c[k].y),
+                            __builtin_fmaf(-pa.z, sn[k].z, me.z * c[k].z), __builtin_fmaf(-pa.w, sn[k].w, me.w * c[k].w));
+      else
+        xr[k] = make_float4(__builtin_fmaf(me.x, c[k].x, pa.x * sn[k].x), __builtin_fmaf(me.y, c[k].y, pa.y * sn[k].y),
+                            __builtin_fmaf(me.z, c[k].z, pa.z * sn[k].z), __builtin_fmaf(me.w, c[k].w, pa.w * sn[k].w));
+    }
+  }
+  if (rot) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) xn[k] = xr[k];
+  }
+  if (live) {
+    if (!S.cache || S.keep_f32) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) st_stream4(x + 32 * k, xn[k]);
+    }
+    if (S.cache) {
+      uint16_t *kc = S.cache + (size_t)tt * (size_t)S.cache_stride + in_head;
+#pragma unroll
+      for (int k = 0; k < K; ++k) st_stream_u2(reinterpret_cast<uint32_t *>(kc + 32 * k), pack4_f16(xn[k]));
+    }
+  }
+}
+
 template <int K>
-static void launch_k(const RopeArgs &a, hipStream_t stream) {
+static void launch_k(const RopeArgs &a, bool flat, hipStream_t stream) {
+  if constexpr (K <= 7) {
+    if (flat && a.n_waves < (1u << 26)) {  // the host's layout: waves per group of 8 tokens
+      bool any_bias = false, norm_and_bias = false;
+      for (int i = 0; i < a.n_sides; ++i) {
+        any_bias = any_bias || a.side[i].bias;
+        norm_and_bias = norm_and_bias || (a.side[i].bias && a.side[i].norm_weight);
+      }
+      const dim3 grid((a.n_waves + 3u) / 4u);
+      if (any_bias && !norm_and_bias)
+        enqueue((rmsnorm_rope_flat_kernel<K, true>), grid, dim3(256), 0, stream, a);
+      else
+        enqueue((rmsnorm_rope_flat_kernel<K, false>), grid, dim3(256), 0, stream, a);
+      return;
+    }
+  }
   if constexpr (K <= 8) {
     // 64 threads per wave index in 32 bits: n_waves < 2^26 (the general kernel covers the rest)
     if (a.n_waves < (1u << 26)) {
@@ -590,13 +754,25 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.n_heads01 = a.n_heads0 + (n_sides > 1 ? sides[1].n_heads : 0);
   a.heads_per_token = a.n_heads01 + (n_sides > 2 ? sides[2].n_heads : 0);
   a.n_heads = (unsigned)n_tokens * (unsigned)a.heads_per_token;
-  // heads per wave: 8 (8 lanes per head), 4 at head_dim 256 (16 lanes per head)
+  // heads per wave: 8 (8 lanes per head), 4 at head_dim 256 (16 lanes per head).  Where a side's
+  // head count is not a multiple of 8 (below head_dim 256), a large call takes the flat layout:
+  // per group of 8 tokens, n_heads waves for each side.  Its waves are full, but each lane group
+  // waits for its own position and the grid has fewer waves, which costs more than the idle lanes
+  // below 1024 tokens (2048 unless half the lanes of the per-token layout would idle).
+  int slots = 0;
+  for (int i = 0; i < n_sides; ++i) slots += (sides[i].n_heads + 7) / 8 * 8;
+  const bool flat = head_dim < 256 && slots != a.heads_per_token &&
+                    (n_tokens >= 2048 || (n_tokens >= 1024 && 2 * a.heads_per_token <= slots));
   const int hpw = head_dim == 256 ? 4 : 8;
-  auto waves = [&](int i) { return i < n_sides ? (sides[i].n_heads + hpw - 1) / hpw : 0; };
+  auto waves = [&](int i) {
+    if (i >= n_sides) return 0;
+    return flat ? sides[i].n_heads : (sides[i].n_heads + hpw - 1) / hpw;
+  };
   a.wave0 = waves(0);
   a.wave01 = a.wave0 + waves(1);
   a.waves_per_token = a.wave01 + waves(2);
-  const unsigned long long n_waves = (unsigned long long)n_tokens * (unsigned long long)a.waves_per_token;
+  const unsigned long long units = flat ? ((unsigned long long)n_tokens + 7) / 8 : (unsigned long long)n_tokens;
+  const unsigned long long n_waves = units * (unsigned long long)a.waves_per_token;
   a.n_waves = n_waves < (1ull << 26) ? (unsigned)n_waves : (1u << 26);  // beyond: the general kernel
   a.head_dim = head_dim;
   a.cos_table = cos_table;
@@ -607,21 +783,21 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.table_rows = table_rows;
   a.eps = eps;
   switch (head_dim / 32) {
-    case 2: launch_k<2>(a, stream); break;
-    case 3: launch_k<3>(a, stream); break;
-    case 4: launch_k<4>(a, stream); break;
-    case 5: launch_k<5>(a, stream); break;
-    case 6: launch_k<6>(a, stream); break;
-    case 7: launch_k<7>(a, stream); break;
-    case 8: launch_k<8>(a, stream); break;
-    case 9: launch_k<9>(a, stream); break;
-    case 10: launch_k<10>(a, stream); break;
-    case 11: launch_k<11>(a, stream); break;
-    case 12: launch_k<12>(a, stream); break;
-    case 13: launch_k<13>(a, stream); break;
-    case 14: launch_k<14>(a, stream); break;
-    case 15: launch_k<15>(a, stream); break;
-    case 16: launch_k<16>(a, stream); break;
+    case 2: launch_k<2>(a, flat, stream); break;
+    case 3: launch_k<3>(a, flat, stream); break;
+    case 4: launch_k<4>(a, flat, stream); break;
+    case 5: launch_k<5>(a, flat, stream); break;
+    case 6: launch_k<6>(a, flat, stream); break;
+    case 7: launch_k<7>(a, flat, stream); break;
+    case 8: launch_k<8>(a, flat, stream); break;
+    case 9: launch_k<9>(a, flat, stream); break;
+    case 10: launch_k<10>(a, flat, stream); break;
+    case 11: launch_k<11>(a, flat, stream); break;
+    case 12: launch_k<12>(a, flat, stream); break;
+    case 13: launch_k<13>(a, flat, stream); break;
+    case 14: launch_k<14>(a, flat, stream); break;
+    case 15: launch_k<15>(a, flat, stream); break;
+    case 16: launch_k<16>(a, flat, stream); break;
     default: break;
   }
 }

@@ -578,7 +578,11 @@ struct ModelShape {
 };
 
 const ModelShape kModels[] = {
+    {"Qwen2.5-0.5B", 896, 14, 2, 64, 4864, 151936, false, true},
+    {"Llama-3.2-1B", 2048, 32, 8, 64, 8192, 128256, false, false},
     {"TinyLlama-1.1B", 2048, 32, 4, 64, 5632, 32000, false, false},
+    {"Qwen2.5-1.5B", 1536, 12, 2, 128, 8960, 151936, false, true},
+    {"Gemma-2-2B", 2304, 8, 4, 256, 9216, 256000, false, false},
     {"Qwen3-4B", 2560, 32, 8, 128, 9728, 151936, true, false},
     {"Phi-3-mini", 3072, 32, 32, 96, 8192, 32064, false, false},
     {"Qwen2.5-7B", 3584, 28, 4, 128, 18944, 152064, false, true},
