@@ -121,8 +121,11 @@ def test_fused_add_rmsnorm_validator_shapes(ops, oracle, dim, seed):
 
 # Model widths: each compiled-in shape of the fixed-length row (2560, 3072, 3584, 3840, 5120, 8192), the run-time
 # thread count with 1, 2 and 4 chunks per thread (1280, 1536 / 6144, 7168 / none below 8192 beyond those), the
-# dispatch shapes (2048, 4096) and a multiple of 256 that falls back to the general kernel (4352).
-MODEL_WIDTHS = [1280, 1536, 2048, 2560, 3072, 3584, 3840, 4096, 4352, 5120, 6144, 7168, 8192]
+# dispatch shapes (2048, 4096) and a multiple of 256 that falls back to the general kernel (4352); below 1024, the
+# 256-thread row at the padded layout and, where the width is not a multiple of 32 (520, 776, 1000), at the natural
+# one (more than 2048 such rows take one wave each: test_one_wave_rows).
+MODEL_WIDTHS = [264, 320, 384, 512, 520, 576, 640, 768, 776, 896, 960, 1000,
+                1280, 1536, 2048, 2560, 3072, 3584, 3840, 4096, 4352, 5120, 6144, 7168, 8192]
 
 
 @pytest.mark.parametrize("dim", MODEL_WIDTHS)
@@ -139,6 +142,37 @@ def test_fused_add_rmsnorm_model_widths(ops, oracle, dim):
     rt = dev(r)
     ops.fused_add_rmsnorm(rt, dev(a), dev(w), eps=1e-6, out=rt)
     assert_bits(host(rt), want_o, f"in-place o dim={dim}")
+
+
+@pytest.mark.parametrize("dim", [264, 320, 448, 512, 520, 576, 640, 768, 776, 896, 960, 1000])
+def test_one_wave_rows(ops, oracle, dim):
+    """More than 2048 rows below 1024 floats: one wave per row with 2, 3 or 4 float4 chunks per lane, full (512,
+    768) and partial, at the padded layout and the natural one (520, 776, 1000), through add+RMSNorm, RMSNorm,
+    RMSNorm -> Q8 and its fused-add form (below 512: the 16-elements-per-thread quantizer starts at 512)."""
+    rows = 2309
+    r = C.normal(dim + 5, (rows, dim))
+    a = C.normal(dim + 6, (rows, dim))
+    w = C.norm_weight(dim + 7, dim)
+    want_o, want_r = oracle.fused_add_rmsnorm(r, a, w, 1e-6)
+    rt = dev(r)
+    got_o = ops.fused_add_rmsnorm(rt, dev(a), dev(w), eps=1e-6)
+    assert_bits(host(rt), want_r, f"residual dim={dim}")
+    assert_bits(host(got_o), want_o, f"o dim={dim}")
+    if dim % 32 == 0:
+        assert_bits(host(ops.rmsnorm(dev(r), dev(w), eps=1e-5)), oracle.rmsnorm(r, w, 1e-5), f"rmsnorm dim={dim}")
+    for gs in (32, 64):
+        if dim % gs or dim >= 512:
+            continue
+        wq, ws = oracle.rmsnorm_quantize(r, w, 1e-6, gs)
+        q, sc = ops.rmsnorm_quantize(dev(r), dev(w), eps=1e-6, gs=gs)
+        assert_bits(host(q), wq, f"codes dim={dim} gs={gs}")
+        assert_bits(host(sc), ws, f"scales dim={dim} gs={gs}")
+        rt = dev(r)
+        q, sc = ops.add_rmsnorm_quantize(rt, dev(a), dev(w), eps=1e-6, gs=gs)
+        wq, ws = oracle.rmsnorm_quantize(want_r, w, 1e-6, gs)
+        assert_bits(host(rt), want_r, f"add residual dim={dim} gs={gs}")
+        assert_bits(host(q), wq, f"add codes dim={dim} gs={gs}")
+        assert_bits(host(sc), ws, f"add scales dim={dim} gs={gs}")
 
 
 def test_fused_add_rmsnorm_out_aliases_residual(ops, oracle):
@@ -556,6 +590,8 @@ def test_rmsnorm_rows(ops, oracle, dim, seed):
 
 @pytest.mark.parametrize("dim", MODEL_WIDTHS)
 def test_rmsnorm_model_widths(ops, oracle, dim):
+    if dim % 32:
+        pytest.skip("RMSNorm takes whole 32-float blocks")
     rows = 37
     x = C.normal(dim + 3, (rows, dim), 2.0)
     w = C.norm_weight(dim + 4, dim)
@@ -567,8 +603,8 @@ def test_rmsnorm_model_widths(ops, oracle, dim):
 
 
 @pytest.mark.parametrize("gs", [64, 32])
-@pytest.mark.parametrize("dim", [64, 128, 512, 544, 1024, 2048, 2560, 3072, 3584, 3840, 4096, 5120, 6144, 7168, 8192,
-                                 12288, 16384])
+@pytest.mark.parametrize("dim", [64, 128, 192, 320, 384, 448, 512, 544, 1024, 2048, 2560, 3072, 3584, 3840, 4096,
+                                 5120, 6144, 7168, 8192, 12288, 16384])
 def test_rmsnorm_quantize_rows(ops, oracle, gs, dim):
     if dim % gs:
         pytest.skip("dim must be a multiple of the group size")
@@ -582,7 +618,7 @@ def test_rmsnorm_quantize_rows(ops, oracle, gs, dim):
 
 
 @pytest.mark.parametrize("gs", [64, 32])
-@pytest.mark.parametrize("dim", [64, 2048, 2560, 3072, 3584, 3840, 4096, 5120, 6144, 8192, 12288])
+@pytest.mark.parametrize("dim", [64, 320, 448, 2048, 2560, 3072, 3584, 3840, 4096, 5120, 6144, 8192, 12288])
 def test_add_rmsnorm_quantize_equals_the_two_calls(ops, oracle, gs, dim):
     """The fused decode step equals v7s_add_inplace then v7s_rmsnorm_quantize (src/asm/forward_q8.inc:386-387)."""
     rows = 9

@@ -70,6 +70,27 @@ def test_sweep_fused_add_rmsnorm(ops, oracle):
         assert same(got_o, want_o) and same(host(rt), want_r), (rows, dim, eps)
 
 
+def test_sweep_one_wave_rows(ops, oracle):
+    """More than 2048 rows of 264 to 1016 floats (one wave per row), a quarter of the cases: add+RMSNorm at every
+    width % 8, RMSNorm and RMSNorm -> Q8 at width % 64."""
+    def draw(r):
+        return int(r.integers(2049, 3001)), 8 * int(r.integers(33, 128)), int(r.choice([32, 64]))
+
+    for rows, dim, gs in shapes("wave_rows", draw)[:max(1, CASES // 4)]:
+        res = C.normal(rows + dim, (rows, dim))
+        add = C.normal(rows + dim + 1, (rows, dim))
+        w = C.norm_weight(dim + 9, dim)
+        want_o, want_r = oracle.fused_add_rmsnorm(res, add, w, 1e-6)
+        rt = dev(res)
+        got_o = host(ops.fused_add_rmsnorm(rt, dev(add), dev(w), eps=1e-6))
+        assert same(got_o, want_o) and same(host(rt), want_r), (rows, dim)
+        if dim % 64 == 0:
+            assert same(host(ops.rmsnorm(dev(res), dev(w), eps=1e-6)), oracle.rmsnorm(res, w, 1e-6)), (rows, dim)
+            wq, ws = oracle.rmsnorm_quantize(res, w, 1e-6, gs)
+            gq, gsc = ops.rmsnorm_quantize(dev(res), dev(w), eps=1e-6, gs=gs)
+            assert same(host(gq), wq) and same(host(gsc), ws), (rows, dim, gs)
+
+
 def test_sweep_rmsnorm_and_quantize(ops, oracle):
     for rows, dim, gs, eps in shapes("rmsq", lambda r: (int(r.integers(1, 40)), 64 * int(r.integers(1, 257)),
                                                         int(r.choice([32, 64])), float(r.choice([1e-6, 1e-5])))):
