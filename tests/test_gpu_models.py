@@ -1,12 +1,12 @@
 """The four per-layer kernels at the model shapes of the load test's `models` mode (csrc/v7g_loadtest.cpp
-kModels: the published widths, head counts, head_dims, QKV bias / Q-K norm and intermediate sizes of twelve
+kModels: the published widths, head counts, head_dims, QKV bias / Q-K norm and intermediate sizes of fourteen
 open-weight models), bit for bit against the oracle: the Q8 embedding gather (a small vocabulary at the model's
 width), add+RMSNorm over the width, the Q/K step inside the fused QKV row (RMSNorm+RoPE with Q/K norms, else RoPE
 only with the QKV bias added to Q, K and V first where the model has one, and the K/V binary16 cache rows), and
 SwiGLU -> Q8 over the intermediate size (32-element groups).  11 tokens, 2053 for the Q/K step.  Every
 shape-specific launch the library picks for these shapes (the fixed-length add+RMSNorm rows, embedding blocks sized
 to the row, the bias through the weight registers, 16 lanes per head at head_dim 256, the flat layout for head
-counts that are not multiples of 8) runs here."""
+counts that are not multiples of a wave's heads) runs here."""
 from __future__ import annotations
 
 import numpy as np
@@ -21,6 +21,8 @@ torch = pytest.importorskip("torch")
 # name, dim, q heads, kv heads, head_dim, hidden, Q/K norm, QKV bias (the load test's model table)
 MODELS = [
     ("Qwen2.5-0.5B", 896, 14, 2, 64, 4864, False, True),
+    ("Qwen3-0.6B", 1024, 16, 8, 128, 3072, True, False),
+    ("Gemma-3-1B", 1152, 4, 1, 256, 6912, True, False),
     ("Llama-3.2-1B", 2048, 32, 8, 64, 8192, False, False),
     ("TinyLlama-1.1B", 2048, 32, 4, 64, 5632, False, False),
     ("Qwen2.5-1.5B", 1536, 12, 2, 128, 8960, False, True),

@@ -299,12 +299,16 @@ def test_qk_rmsnorm_rope_partial_waves(ops, oracle, Hq, Hk, D):
     (2055, 7, 1, 96, True, False, True, True, 5),         # odd head_dim / 32, positions pos0 + t
     (2050, 3, 3, 160, False, False, True, True, None),
     (2051, 12, 4, 192, False, True, True, True, None),
-    (2053, 5, 2, 224, True, True, False, False, None)])
+    (2053, 5, 2, 224, True, True, False, False, None),
+    (2049, 4, 1, 256, True, False, True, True, None),     # Gemma-3-1B: 16 lanes per head, 4 pairs per wave
+    (1030, 1, 1, 256, False, True, True, False, None),
+    (2051, 6, 3, 256, True, True, False, True, 7)])
 def test_qkv_stage_flat_layout(ops, oracle, T, nq, nkv, hd, norm, bias, keep_k, keep_v, pos0):
-    """From 1024 or 2048 tokens, head counts that are not multiples of 8 below head_dim 256 take the flat layout
-    (8 (token, head) pairs of one side per wave, tokens in groups of 8, each lane group with its own position):
-    last groups of fewer than 8 tokens, positions 0 (no rotation) and past the tables (NaN in Q and K, V kept),
-    every head_dim / 32 from 2 to 7, bias or norm weight or both, cache rows with and without the f32 result."""
+    """From 1024 or 2048 tokens, head counts that are not multiples of a wave's heads take the flat layout (8
+    (token, head) pairs of one side per wave over groups of 8 tokens, 4 over groups of 4 at head_dim 256; each lane
+    group with its own position): last groups of fewer tokens, positions 0 (no rotation) and past the tables (NaN
+    in Q and K, V kept), every head_dim / 32 from 2 to 8, bias or norm weight or both, cache rows with and without
+    the f32 result."""
     s = T + 7 * nq + hd
     qkv = C.normal(s, (T, (nq + 2 * nkv) * hd))
     qw, kw = C.norm_weight(s + 1, hd), C.norm_weight(s + 2, hd)

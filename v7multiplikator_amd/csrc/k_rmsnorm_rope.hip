@@ -43,7 +43,8 @@ struct RopeArgs {
   int heads_per_token;      // heads of all sides
   unsigned n_heads;         // n_tokens * heads_per_token
   // The wave kernels' grid: per token, ceil(heads / 8) waves for each side (heads / 4 at head_dim 256);
-  // the flat kernel's: per group of 8 tokens, heads waves for each side (waves_per_token then counts a group).
+  // the flat layout's: per group of 8 tokens (4 at head_dim 256), heads waves for each side
+  // (waves_per_token then counts a group).
   int wave0, wave01;        // side 0 waves; sides 0 + 1 waves
   int waves_per_token;
   unsigned n_waves;         // n_tokens * waves_per_token
@@ -430,7 +431,12 @@ __device__ __forceinline__ float ror8_f(float v) {  // lane l gets lane l ^ 8 of
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
 }
 
-template <bool BW>
+// FLAT (head counts that are not multiples of 4, from 1024 tokens): tokens go
+// in groups of 4 and each side's (token, head) pairs of a group are dealt out
+// 4 to a wave in token-major order (side s: n_s waves per group), as the flat
+// layout of the 8-lane kernel below; the position, the table rows, the
+// out-of-table NaN and the rotation are then per 16-lane group.
+template <bool BW, bool FLAT = false>
 __global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave16_kernel(RopeArgs a) {
   constexpr int HD = 256;
   const int m = threadIdx.x & 7;
@@ -439,16 +445,30 @@ __global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave16_kernel(RopeArgs a)
   const unsigned wi = __builtin_amdgcn_readfirstlane((blockIdx.x * 256u + threadIdx.x) >> 6);  // wave index
   const bool live_wave = wi < a.n_waves;
   const unsigned wvv = live_wave ? wi : 0u;
-  const unsigned t = wvv / (unsigned)a.waves_per_token;
-  const int r = (int)(wvv - t * (unsigned)a.waves_per_token);
+  const unsigned grp = wvv / (unsigned)a.waves_per_token;  // the token, or with FLAT the group of 4 tokens
+  const int r = (int)(wvv - grp * (unsigned)a.waves_per_token);
   const int sd = r < a.wave0 ? 0 : (r < a.wave01 ? 1 : 2);
   const RopeSide &S = a.side[sd];
   const int hs_raw = 4 * (r - (sd == 0 ? 0 : (sd == 1 ? a.wave0 : a.wave01))) + ((threadIdx.x & 63) >> 4);
-  const bool live = live_wave && hs_raw < S.n_heads;
-  const int hs = hs_raw < S.n_heads ? hs_raw : S.n_heads - 1;
+  bool live;
+  int hs;
+  unsigned t;
+  if constexpr (FLAT) {  // hs_raw is the pair's index among the side's 4 * n_heads pairs of the group
+    const unsigned n_tokens = a.n_heads / (unsigned)a.heads_per_token;
+    const unsigned tl = (unsigned)hs_raw / (unsigned)S.n_heads;
+    hs = hs_raw - (int)(tl * (unsigned)S.n_heads);
+    const unsigned tg = 4u * grp + tl;
+    live = live_wave && tg < n_tokens;
+    t = tg < n_tokens ? tg : n_tokens - 1;
+  } else {
+    live = live_wave && hs_raw < S.n_heads;
+    hs = hs_raw < S.n_heads ? hs_raw : S.n_heads - 1;
+    t = grp;
+  }
+  int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
+  if constexpr (FLAT) asm volatile("" ::: "memory");  // the position's load goes out ahead of the head's
   const size_t in_head = (size_t)hs * HD + lane_off;
   float *x = S.buf + (size_t)t * (size_t)S.token_stride + in_head;
-  int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
   // A position outside the tables cannot be read: its rotated heads become NaN.
   const bool bad_pos = S.rotate && pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
   if (bad_pos) pos = 0;
@@ -723,7 +743,10 @@ static void launch_k(const RopeArgs &a, bool flat, hipStream_t stream) {
       const bool bw = any_bias && !norm_and_bias;
       const dim3 grid((a.n_waves + 3u) / 4u);
       if constexpr (K == 8) {  // head_dim 256: 4 heads per wave (the host's wave layout)
-        if (bw)
+        if (flat)
+          bw ? enqueue((rmsnorm_rope_wave16_kernel<true, true>), grid, dim3(256), 0, stream, a)
+             : enqueue((rmsnorm_rope_wave16_kernel<false, true>), grid, dim3(256), 0, stream, a);
+        else if (bw)
           enqueue((rmsnorm_rope_wave16_kernel<true>), grid, dim3(256), 0, stream, a);
         else
           enqueue((rmsnorm_rope_wave16_kernel<false>), grid, dim3(256), 0, stream, a);
@@ -755,15 +778,15 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.heads_per_token = a.n_heads01 + (n_sides > 2 ? sides[2].n_heads : 0);
   a.n_heads = (unsigned)n_tokens * (unsigned)a.heads_per_token;
   // heads per wave: 8 (8 lanes per head), 4 at head_dim 256 (16 lanes per head).  Where a side's
-  // head count is not a multiple of 8 (below head_dim 256), a large call takes the flat layout:
-  // per group of 8 tokens, n_heads waves for each side.  Its waves are full, but each lane group
-  // waits for its own position and the grid has fewer waves, which costs more than the idle lanes
-  // below 1024 tokens (2048 unless half the lanes of the per-token layout would idle).
-  int slots = 0;
-  for (int i = 0; i < n_sides; ++i) slots += (sides[i].n_heads + 7) / 8 * 8;
-  const bool flat = head_dim < 256 && slots != a.heads_per_token &&
-                    (n_tokens >= 2048 || (n_tokens >= 1024 && 2 * a.heads_per_token <= slots));
+  // head count is not a multiple of that (up to head_dim 256), a large call takes the flat layout:
+  // per group of 8 (4) tokens, n_heads waves for each side.  Its waves are full, but each lane
+  // group waits for its own position and the grid has fewer waves, which costs more than the idle
+  // lanes below 1024 tokens (2048 unless half the lanes of the per-token layout would idle).
   const int hpw = head_dim == 256 ? 4 : 8;
+  int slots = 0;
+  for (int i = 0; i < n_sides; ++i) slots += (sides[i].n_heads + hpw - 1) / hpw * hpw;
+  const bool flat = head_dim <= 256 && slots != a.heads_per_token &&
+                    (n_tokens >= 2048 || (n_tokens >= 1024 && 2 * a.heads_per_token <= slots));
   auto waves = [&](int i) {
     if (i >= n_sides) return 0;
     return flat ? sides[i].n_heads : (sides[i].n_heads + hpw - 1) / hpw;
@@ -771,7 +794,8 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.wave0 = waves(0);
   a.wave01 = a.wave0 + waves(1);
   a.waves_per_token = a.wave01 + waves(2);
-  const unsigned long long units = flat ? ((unsigned long long)n_tokens + 7) / 8 : (unsigned long long)n_tokens;
+  const unsigned long long units =
+      flat ? ((unsigned long long)n_tokens + hpw - 1) / hpw : (unsigned long long)n_tokens;
   const unsigned long long n_waves = units * (unsigned long long)a.waves_per_token;
   a.n_waves = n_waves < (1ull << 26) ? (unsigned)n_waves : (1u << 26);  // beyond: the general kernel
   a.head_dim = head_dim;

@@ -579,6 +579,8 @@ struct ModelShape {
 
 const ModelShape kModels[] = {
     {"Qwen2.5-0.5B", 896, 14, 2, 64, 4864, 151936, false, true},
+    {"Qwen3-0.6B", 1024, 16, 8, 128, 3072, 151936, true, false},
+    {"Gemma-3-1B", 1152, 4, 1, 256, 6912, 262144, true, false},
     {"Llama-3.2-1B", 2048, 32, 8, 64, 8192, 128256, false, false},
     {"TinyLlama-1.1B", 2048, 32, 4, 64, 5632, 32000, false, false},
     {"Qwen2.5-1.5B", 1536, 12, 2, 128, 8960, 151936, false, true},
