@@ -1,5 +1,6 @@
-"""The loader a v7 host would add compiles as C11 against include/v7g_lib.h and
-resolves every entry it lists from the built libv7g.so (dlopen/dlsym only: no GPU call is made)."""
+"""The loader a v7 host would add (the C block of the repository's integration guide) compiles as C11 against
+include/v7g_lib.h and resolves every entry it lists from the built libv7g.so (dlopen/dlsym only: no GPU call is
+made)."""
 from __future__ import annotations
 
 import os
