@@ -27,10 +27,13 @@
 // happens in registers; otherwise it is in lane m ^ 4 (the wave kernel's
 // lane exchange) or goes through LDS (the per-lane kernel).  At head_dim 256
 // a head spans 16 lanes, the two halves holding alternate blocks, and the
-// chains pass from one half to the other after each block (same order).  Heads are read and written in place with streaming
-// loads and stores (the norm weights and the cos/sin rows, shared by every
-// head of a token, stay cached).  The result is bit-identical to the
-// reference.
+// chains pass from one half to the other after each block (same order).  A
+// wave holds heads of one side of one token, or, where a side's head count
+// does not fill whole waves and the call is large, (token, head) pairs of one
+// side over a group of tokens (the flat layout).  Heads are read and written
+// in place with streaming loads and stores (the norm weights and the cos/sin
+// rows, shared by every head of a token, stay cached).  The result is
+// bit-identical to the reference.
 #include "v7g_device.h"
 #include "v7g_internal.h"
 
@@ -570,9 +573,9 @@ __global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave16_kernel(RopeArgs a)
 // Head counts that are not multiples of 8 (2 KV heads, 12, 14 or 28 Q heads),
 // from 1024 tokens: rmsnorm_rope_wave_kernel's last wave of such a side holds
 // only its leftover heads, and its idle lanes still issue every instruction (a
-// side of 2 heads fills a quarter of its wave).  Here tokens go in groups of 8 and each side's
-// (token, head) pairs of a group are dealt out 8 to a wave in token-major
-// order, so every wave is full: side s takes n_s waves per group, and lane
+// side of 2 heads fills a quarter of its wave).  Here tokens go in groups of
+// 8 and each side's (token, head) pairs of a group are dealt out 8 to a wave
+// in token-major order, so every wave is full: side s takes n_s waves per group, and lane
 // group g of wave j holds pair 8j + g, i.e. token 8*group + (8j + g) / n_s,
 // head (8j + g) % n_s.  The side's descriptor stays wave-uniform; the position
 // is per lane (its load goes out first, so the wait for it covers no other
