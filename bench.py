@@ -26,6 +26,12 @@ chain kernels (add+RMSNorm, Q/K RMSNorm+RoPE) on the same sample, beside the
 restatement's same two kernels and checked against them bit for bit
 (V7_REF_EPS: the eps its g_rms_eps global holds, 0 without its database init).
 
+`rows` times the widened rows of the path at the same shapes, after the timed region and outside `value`
+(RMSNorm -> Q8, its fused residual-add form, the K/V pack, the Q/K/V stage with binary16 cache rows, the
+QKV-bias RoPE-only stage, add_inplace), each call timed like the chain's kernels; `cpu_baseline.rows` times
+the restatement of each row on the host, one call per token row over the host threads, and checks the
+GPU's outputs for the same inputs bit for bit.
+
     python bench.py [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
 """
 from __future__ import annotations
@@ -59,6 +65,36 @@ BYTES = {
     "swiglu_q8": 2 * T * HIDDEN * 4 + T * HIDDEN + T * (HIDDEN // GS) * 4,
 }
 DOMINANT = "swiglu_q8"
+
+# The widened rows of the path at the same shapes (not part of `value`): bytes per call over T tokens.
+QKV = (NQ + 2 * NKV) * HD
+KVD = NKV * HD
+ROW_BYTES = {
+    "rmsnorm_quantize": T * DIM * 4 + T * DIM + T * (DIM // 64) * 4 + DIM * 4,
+    "add_rmsnorm_quantize": 3 * T * DIM * 4 + T * DIM + T * (DIM // 64) * 4 + DIM * 4,
+    "kv_pack_f16_kv": 2 * T * KVD * 4 + 2 * T * KVD * 2,
+    "qkv_rope_stage": T * QKV * 4 + T * NQ * HD * 4 + 2 * T * KVD * 2 + 2 * T * (HD // 2) * 4 + 2 * HD * 4,
+    "qkv_bias_rope_only": 2 * T * QKV * 4 + QKV * 4 + 2 * T * (HD // 2) * 4,
+    "add_inplace": 3 * T * DIM * 4,
+}
+ROW_SHAPES = {
+    "rmsnorm_quantize": "RMSNorm -> Q8 [8192, 4096], GS 64",
+    "add_rmsnorm_quantize": "residual add then RMSNorm -> Q8 [8192, 4096], GS 64, one pass",
+    "kv_pack_f16_kv": "K and V rows of the QKV row to binary16 cache rows, 8192 tokens x 1024, one launch",
+    "qkv_rope_stage": "Q/K RMSNorm+RoPE 32 + 8 heads of 128, K/V to binary16 cache rows, f32 Q kept, 8192 tokens",
+    "qkv_bias_rope_only": "QKV bias on Q, K, V then RoPE only on Q and K, 32 + 8 + 8 heads of 128, 8192 tokens",
+    "add_inplace": "x += y over [8192, 4096]",
+}
+ROW_FORMS = {  # the restatement each row's CPU timing runs (oracle/)
+    "rmsnorm_quantize": "scalar C restatement",
+    "add_rmsnorm_quantize": "scalar C restatement",
+    "kv_pack_f16_kv": "F16C vcvtps2ph, the reference's instruction",
+    "qkv_rope_stage": "AVX2 RMSNorm+RoPE restatement and the F16C pack",
+    "qkv_bias_rope_only": "scalar C restatement",
+    "add_inplace": "scalar C restatement",
+}
+ROW_KINDS = {"rmsnorm_quantize": 0, "add_rmsnorm_quantize": 1, "kv_pack_f16_kv": 2, "qkv_rope_stage": 3,
+             "qkv_bias_rope_only": 4, "add_inplace": 5}  # orc_rows_args.kind (oracle/v7_oracle.h)
 
 
 def parse():
@@ -133,6 +169,67 @@ class Chain:
         ]
 
 
+class RowData:
+    """Inputs of the widened rows over n tokens at the chain's shapes (the QKV rows carry Q, K and V heads)."""
+
+    def __init__(self, torch, n, seed, device):
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        f32 = torch.float32
+        self.x = torch.randn((n, DIM), generator=g, dtype=f32, device=device)
+        self.add = torch.randn((n, DIM), generator=g, dtype=f32, device=device)
+        self.w = 1.0 + 0.1 * torch.randn(DIM, generator=g, dtype=f32, device=device)
+        self.qkv = torch.randn((n, QKV), generator=g, dtype=f32, device=device)
+        self.bias = 0.5 * torch.randn(QKV, generator=g, dtype=f32, device=device)
+        self.q_w = 1.0 + 0.1 * torch.randn(HD, generator=g, dtype=f32, device=device)
+        self.k_w = 1.0 + 0.1 * torch.randn(HD, generator=g, dtype=f32, device=device)
+        self.positions = torch.arange(n, dtype=torch.int32, device=device)
+
+
+class Rows:
+    """Device buffers of the widened rows (two sets, used in turn, so that no call finds its inputs in the
+    Infinity Cache) and one launch per row."""
+
+    def __init__(self, torch, ops, chain, seed):
+        self.ops, self.cos, self.sin = ops, chain.cos, chain.sin
+        self.sets = []
+        for i in range(2):
+            d = RowData(torch, T, seed + 100 + i, "cuda")
+            d.codes = torch.empty((T, DIM), dtype=torch.int8, device="cuda")
+            d.scales = torch.empty((T, DIM // 64), dtype=torch.float32, device="cuda")
+            d.kc = torch.empty((T, KVD), dtype=torch.float16, device="cuda")
+            d.vc = torch.empty((T, KVD), dtype=torch.float16, device="cuda")
+            self.sets.append(d)
+
+    def launch(self, name, d):
+        return row_call(self.ops, name, d, self.cos, self.sin, d.codes, d.scales, d.kc, d.vc)
+
+
+def row_call(ops, name, d, cos, sin, codes, scales, kc, vc):
+    """One call of row `name` on the inputs d (updated in place where the row works in place)."""
+    n = d.x.shape[0]
+    q = d.qkv[:, :NQ * HD].view(n, NQ, HD)
+    k = d.qkv[:, NQ * HD:(NQ + NKV) * HD].view(n, NKV, HD)
+    v = d.qkv[:, (NQ + NKV) * HD:].view(n, NKV, HD)
+    if name == "rmsnorm_quantize":
+        ops.rmsnorm_quantize(d.x, d.w, eps=EPS, gs=64, out_q=codes, out_s=scales)
+    elif name == "add_rmsnorm_quantize":
+        ops.add_rmsnorm_quantize(d.x, d.add, d.w, eps=EPS, gs=64, out_q=codes, out_s=scales)
+    elif name == "kv_pack_f16_kv":
+        ops.kv_pack_f16_kv(d.qkv[:, NQ * HD:(NQ + NKV) * HD], d.qkv[:, (NQ + NKV) * HD:], k_out=kc, v_out=vc)
+    elif name == "qkv_rope_stage":
+        ops.qkv_rope_stage(q, k, v, cos, sin, positions=d.positions, eps=EPS, q_norm_weight=d.q_w,
+                           k_norm_weight=d.k_w, k_cache=kc.view(n, NKV, HD), v_cache=vc.view(n, NKV, HD),
+                           keep_k_f32=False, keep_v_f32=False)
+    elif name == "qkv_bias_rope_only":
+        ops.qkv_rope_stage(q, k, v, cos, sin, positions=d.positions, eps=EPS, q_bias=d.bias[:NQ * HD],
+                           k_bias=d.bias[NQ * HD:(NQ + NKV) * HD], v_bias=d.bias[(NQ + NKV) * HD:])
+    elif name == "add_inplace":
+        ops.add_inplace(d.x, d.add)
+    else:
+        raise ValueError(name)
+
+
 class ChainArgs(ctypes.Structure):
     """orc_chain_args (oracle/v7_oracle.h): shapes, eps and the host buffers of one chain sample."""
     _fields_ = [(n, ctypes.c_int) for n in
@@ -141,6 +238,98 @@ class ChainArgs(ctypes.Structure):
                                     ("ids", "positions", "table_q", "table_s", "emb_out", "residual", "add",
                                      "w_norm", "normed", "q", "k", "q_w", "k_w", "cos_table", "sin_table",
                                      "gate", "up", "act", "codes", "scales")]
+
+
+class RowsArgs(ctypes.Structure):
+    """orc_rows_args (oracle/v7_oracle.h): the kind, shapes, eps and host buffers of one widened row."""
+    _fields_ = [(n, ctypes.c_int) for n in
+                ("kind", "n_tokens", "dim", "gs", "n_q_heads", "n_kv_heads", "head_dim", "rope_max_dim")] + [
+        ("eps", ctypes.c_float), ("x", ctypes.c_void_p), ("add", ctypes.c_void_p), ("weight", ctypes.c_void_p),
+        ("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("qkv", ctypes.c_void_p),
+        ("qkv_stride", ctypes.c_longlong)] + [(n, ctypes.c_void_p) for n in
+                                              ("q_w", "k_w", "bias", "cos_table", "sin_table", "positions",
+                                               "k_cache", "v_cache")]
+
+
+def rows_leg(torch, ops, chain, L, cores, seconds):
+    """The widened rows on the host: the restatement driven per token row over `cores` threads
+    (orc_rows_bench, oracle/v7_oracle_rows.c) over all T tokens, and the GPU's outputs of the same inputs
+    compared bit for bit (codes, scales, updated rows, cache rows)."""
+    import numpy as np
+
+    hostc = lambda t: np.ascontiguousarray(t.detach().cpu().numpy())  # noqa: E731
+    L.orc_rows_bench.restype = ctypes.c_double
+    L.orc_rows_bench.argtypes = [ctypes.POINTER(RowsArgs), ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    src = RowData(torch, T, 7, "cuda")
+    h = {k: hostc(getattr(src, k)) for k in ("x", "add", "w", "qkv", "bias", "q_w", "k_w", "positions")}
+    cos_t, sin_t = hostc(chain.cos), hostc(chain.sin)
+    out = {}
+    # the buffers a row touches, per copy: the repetitions cycle through enough copies to span 1.5 GB, more
+    # than the host's caches hold
+    touched = {"rmsnorm_quantize": ("x", "codes"), "add_rmsnorm_quantize": ("x", "add", "codes"),
+               "kv_pack_f16_kv": ("qkv", "kc", "vc"), "qkv_rope_stage": ("qkv", "kc", "vc"),
+               "qkv_bias_rope_only": ("qkv",), "add_inplace": ("x", "add")}
+    for name, kind in ROW_KINDS.items():
+        def copy_set():  # fresh copies of what the row reads or writes; the rest is shared
+            b = {k: (v.copy() if k in touched[name] else v) for k, v in h.items()}
+            b["codes"] = np.zeros((T, DIM), np.int8)
+            b["scales"] = np.zeros((T, DIM // 64), np.float32)
+            b["kc"] = np.zeros((T, KVD), np.uint16)
+            b["vc"] = np.zeros((T, KVD), np.uint16)
+            return b
+
+        def args_of(b):
+            p = lambda a: a.ctypes.data  # noqa: E731
+            return RowsArgs(kind, T, DIM, 64, NQ, NKV, HD, HD // 2, EPS, p(b["x"]), p(b["add"]), p(b["w"]),
+                            p(b["codes"]), p(b["scales"]), p(b["qkv"]), QKV, p(b["q_w"]), p(b["k_w"]), p(b["bias"]),
+                            p(cos_t), p(sin_t), p(b["positions"]), p(b["kc"]), p(b["vc"]))
+
+        b = copy_set()
+        a = args_of(b)
+        L.orc_rows_bench(ctypes.byref(a), 1, cores, 1)
+        # the GPU on the same inputs
+        d = RowData.__new__(RowData)
+        for k in ("x", "add", "w", "qkv", "bias", "q_w", "k_w", "positions"):
+            setattr(d, k, getattr(src, k).clone())
+        codes = torch.zeros((T, DIM), dtype=torch.int8, device="cuda")
+        scales = torch.zeros((T, DIM // 64), dtype=torch.float32, device="cuda")
+        kc = torch.zeros((T, KVD), dtype=torch.float16, device="cuda")
+        vc = torch.zeros((T, KVD), dtype=torch.float16, device="cuda")
+        row_call(ops, name, d, chain.cos, chain.sin, codes, scales, kc, vc)
+        torch.cuda.synchronize()
+        if name in ("rmsnorm_quantize", "add_rmsnorm_quantize"):
+            same = np.array_equal(hostc(codes), b["codes"]) and np.array_equal(hostc(scales), b["scales"])
+            same = same and np.array_equal(hostc(d.x), b["x"])
+        elif name == "add_inplace":
+            same = np.array_equal(hostc(d.x), b["x"])
+        elif name == "kv_pack_f16_kv":
+            same = np.array_equal(hostc(kc).view(np.uint16), b["kc"]) and np.array_equal(hostc(vc).view(np.uint16),
+                                                                                          b["vc"])
+        elif name == "qkv_rope_stage":
+            same = (np.array_equal(hostc(d.qkv)[:, :NQ * HD], b["qkv"][:, :NQ * HD])
+                    and np.array_equal(hostc(kc).view(np.uint16), b["kc"])
+                    and np.array_equal(hostc(vc).view(np.uint16), b["vc"]))
+        else:
+            same = np.array_equal(hostc(d.qkv).view(np.uint32), b["qkv"].view(np.uint32))
+        del d, codes, scales, kc, vc
+        per_set = sum(b[k].nbytes for k in touched[name])
+        sets = [b] + [copy_set() for _ in range(max(1, -(-1_500_000_000 // per_set)) - 1)]
+        arr = (RowsArgs * len(sets))(*[args_of(x) for x in sets])
+        L.orc_rows_bench(arr, len(sets), cores, len(sets))  # one warm pass over every copy
+        # timing: rounds of whole passes over the copies until `seconds` of work have been timed
+        secs, reps, chunk = 0.0, 0, len(sets)
+        while secs < seconds:
+            t = L.orc_rows_bench(arr, len(sets), cores, chunk)
+            secs += t
+            reps += chunk
+            chunk = len(sets) * max(1, min(4 * chunk // len(sets),
+                                           int((seconds - secs) / max(t / chunk, 1e-6)) // len(sets) + 1))
+        out[name] = {"value": round(ROW_BYTES[name] * reps / secs / 1e9, 3), "unit": "GB/s", "cores": cores,
+                     "kind": "port", "form": ROW_FORMS[name], "gpu_bit_exact": bool(same),
+                     "sample": f"all {T} tokens, per-row calls, {reps} repetitions in {secs:.1f} s cycling "
+                               f"through {len(sets)} copies of the buffers ({len(sets) * per_set / 1e9:.1f} GB)"}
+        del sets, arr, b
+    return out
 
 
 def cpu_baseline(torch, ops, chain, args):
@@ -236,6 +425,7 @@ def cpu_baseline(torch, ops, chain, args):
     # sample (the same rows, still beyond the host caches) for a quarter of the time.
     n1 = max(1, S // 4)
     gbs1, reps1, secs1 = timed(1, n1, args.cpu_seconds / 4)
+    rows = rows_leg(torch, ops, chain, L, cores, max(0.5, args.cpu_seconds / 10))
     ref_so = os.environ.get("V7_REF_SO")
     reference = None
     if ref_so:
@@ -251,6 +441,7 @@ def cpu_baseline(torch, ops, chain, args):
                           "sample": f"{n1} tokens, {reps1} repetitions in {secs1:.1f} s"},
         "cpu_model": cpu_model(),
         "gpu_sample_bit_exact": match,
+        "rows": rows,
         **({"reference": reference} if reference is not None else {}),
     }
 
@@ -412,6 +603,26 @@ def main():
             fn()
     torch.cuda.synchronize()
 
+    # The widened rows at the same shapes (after the timed region, not part of `value`): each row's calls
+    # timed the same way, alternating two buffer sets.
+    rows = Rows(torch, ops, chain, args.seed)
+    row_reps = max(4, min(args.steps, 20))
+    rows_out = {}
+    for name in ROW_BYTES:
+        for d in rows.sets:
+            rows.launch(name, d)
+        evr = [(hip.create(), hip.create()) for _ in range(row_reps)]
+        torch.cuda.synchronize()
+        for i in range(row_reps):
+            lib.v7g_time_next_call(*evr[i])
+            rows.launch(name, rows.sets[i % 2])
+        torch.cuda.synchronize()
+        ms = sum(hip.elapsed_ms(a, b) for a, b in evr) / row_reps
+        gbs = ROW_BYTES[name] / (ms * 1e-3) / 1e9
+        rows_out[name] = {"shape": ROW_SHAPES[name], "bytes": ROW_BYTES[name], "us": round(ms * 1e3, 2),
+                          "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del rows
+
     kern = {}
     for i, (name, _) in enumerate(launches):
         ms = sum(hip.elapsed_ms(*evk[s][i]) for s in range(args.steps)) / args.steps
@@ -449,6 +660,7 @@ def main():
                      "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "us_per_launch": round(dom_ms * 1e3, 2), "algorithmic_bytes": BYTES[DOMINANT]},
         "kernels": kern,
+        "rows": rows_out,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -134,6 +134,41 @@ typedef struct orc_chain_args {
  * n_threads host threads.  Returns wall seconds. */
 double orc_avx2_chain_bench(const orc_chain_args *a, int n_threads, int reps);
 
+/* The widened rows, timed per token row over host threads as the reference engine drives them
+ * (v7_oracle_rows.c).  All buffers host memory; the QKV rows are [n_tokens, qkv_stride] with Q, K, V
+ * heads in that order; the K/V cache rows are [n_tokens, n_kv_heads * head_dim] binary16. */
+enum {
+    ORC_ROWS_RMSNORM_Q8 = 0,
+    ORC_ROWS_ADD_RMSNORM_Q8 = 1,
+    ORC_ROWS_KV_PACK = 2,
+    ORC_ROWS_QKV_STAGE = 3,
+    ORC_ROWS_QKV_BIAS_ROPE = 4,
+    ORC_ROWS_ADD_INPLACE = 5
+};
+typedef struct orc_rows_args {
+    int kind, n_tokens, dim, gs, n_q_heads, n_kv_heads, head_dim, rope_max_dim;
+    float eps;
+    float *x;
+    const float *add;
+    const float *weight;
+    int8_t *codes;
+    float *scales;
+    float *qkv;
+    long long qkv_stride;
+    const float *q_w;
+    const float *k_w;
+    const float *bias;
+    const float *cos_table;
+    const float *sin_table;
+    const int32_t *positions;
+    uint16_t *k_cache;
+    uint16_t *v_cache;
+} orc_rows_args;
+
+/* Runs `reps` repetitions, repetition r of kind sets[r % n_sets].kind over rows 0..n_tokens-1 of that set's
+ * buffers (every set of one kind and shape), rows split over n_threads threads; returns wall seconds. */
+double orc_rows_bench(const orc_rows_args *sets, int n_sets, int n_threads, int reps);
+
 /* The reference binary as a baseline (v7_ref_leg.c): loads a libv7_threading.so by path and times its
  * two exported chain kernels, v7s_fused_add_rmsnorm and v7s_rmsnorm_rope_heads, per token row. */
 int orc_ref_open(const char *path);

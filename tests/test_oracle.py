@@ -850,3 +850,56 @@ def test_bias_add_exact(oracle):
     x = C.normal(4, (5, 1024))
     b = C.normal(5, 1024)
     assert bits_equal(oracle.bias_add(x, b), (x + b).astype(F))
+
+
+@pytest.mark.parametrize("kind", range(6))
+def test_rows_driver_matches_the_per_function_oracle(oracle, kind):
+    """The per-row timing driver of the benchmark's CPU leg (orc_rows_bench, oracle/v7_oracle_rows.c) computes
+    each widened row exactly as the oracle's own functions do: RMSNorm -> Q8, add then RMSNorm -> Q8, the K/V
+    pack, the Q/K/V stage, QKV bias + RoPE only, add_inplace (13 tokens over 3 threads)."""
+    import ctypes
+
+    import bench
+
+    T, DIM, NQ, NKV, HD, GS, EPS = 13, 256, 4, 2, 64, 64, 1e-6
+    QKV, KVD = (NQ + 2 * NKV) * HD, NKV * HD
+    x, add = C.normal(1, (T, DIM)), C.normal(2, (T, DIM))
+    w = C.norm_weight(3, DIM)
+    qkv = C.normal(4, (T, QKV))
+    bias = C.normal(5, QKV, 0.5)
+    q_w, k_w = C.norm_weight(6, HD), C.norm_weight(7, HD)
+    ct, st = oracle.rope_tables(T + 3, HD, 1e6)
+    pos = (np.arange(T) + 2).astype(np.int32)
+    pos[4] = 0
+    b = dict(x=x.copy(), add=add, w=w, qkv=qkv.copy(), bias=bias, q_w=q_w, k_w=k_w, ct=ct, st=st, pos=pos,
+             codes=np.zeros((T, DIM), np.int8), scales=np.zeros((T, DIM // GS), np.float32),
+             kc=np.zeros((T, KVD), np.uint16), vc=np.zeros((T, KVD), np.uint16))
+    p = lambda a: a.ctypes.data  # noqa: E731
+    a = bench.RowsArgs(kind, T, DIM, GS, NQ, NKV, HD, HD // 2, EPS, p(b["x"]), p(b["add"]), p(b["w"]),
+                       p(b["codes"]), p(b["scales"]), p(b["qkv"]), QKV, p(b["q_w"]), p(b["k_w"]), p(b["bias"]),
+                       p(b["ct"]), p(b["st"]), p(b["pos"]), p(b["kc"]), p(b["vc"]))
+    L = oracle.lib()
+    L.orc_rows_bench.restype = ctypes.c_double
+    L.orc_rows_bench.argtypes = [ctypes.POINTER(bench.RowsArgs), ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    assert L.orc_rows_bench(ctypes.byref(a), 1, 3, 1) >= 0
+    q3 = lambda r: r[:, :NQ * HD].reshape(T, NQ, HD)  # noqa: E731
+    k3 = lambda r: r[:, NQ * HD:(NQ + NKV) * HD].reshape(T, NKV, HD)  # noqa: E731
+    v3 = lambda r: r[:, (NQ + NKV) * HD:].reshape(T, NKV, HD)  # noqa: E731
+    if kind in (0, 1):
+        xs = oracle.add_inplace(x, add) if kind == 1 else x
+        wq, ws = oracle.rmsnorm_quantize(xs, w, EPS, GS)
+        assert bits_equal(b["x"], xs) and np.array_equal(b["codes"], wq) and bits_equal(b["scales"], ws)
+    elif kind == 2:
+        assert np.array_equal(b["kc"], oracle.kv_pack_f16(k3(qkv)).reshape(T, KVD))
+        assert np.array_equal(b["vc"], oracle.kv_pack_f16(v3(qkv)).reshape(T, KVD))
+    elif kind == 3:
+        wq, wk, wv, wkc, wvc = oracle.qkv_stage(q3(qkv), k3(qkv), v3(qkv), q_w, k_w, None, None, None, ct, st, pos,
+                                                EPS)
+        assert bits_equal(q3(b["qkv"]), wq) and bits_equal(k3(b["qkv"]), wk)
+        assert np.array_equal(b["kc"], wkc.reshape(T, KVD)) and np.array_equal(b["vc"], wvc.reshape(T, KVD))
+    elif kind == 4:
+        wq, wk, wv, _, _ = oracle.qkv_stage(q3(qkv), k3(qkv), v3(qkv), None, None, bias[:NQ * HD],
+                                            bias[NQ * HD:(NQ + NKV) * HD], bias[(NQ + NKV) * HD:], ct, st, pos, EPS)
+        assert bits_equal(q3(b["qkv"]), wq) and bits_equal(k3(b["qkv"]), wk) and bits_equal(v3(b["qkv"]), wv)
+    else:
+        assert bits_equal(b["x"], oracle.add_inplace(x, add))
