@@ -86,12 +86,12 @@ ROW_SHAPES = {
     "add_inplace": "x += y over [8192, 4096]",
 }
 ROW_FORMS = {  # the restatement each row's CPU timing runs (oracle/)
-    "rmsnorm_quantize": "scalar C restatement",
-    "add_rmsnorm_quantize": "scalar C restatement",
+    "rmsnorm_quantize": "AVX2 RMSNorm and Q8 quantizer restatement",
+    "add_rmsnorm_quantize": "AVX2 vaddps, RMSNorm and Q8 quantizer restatement",
     "kv_pack_f16_kv": "F16C vcvtps2ph, the reference's instruction",
     "qkv_rope_stage": "AVX2 RMSNorm+RoPE restatement and the F16C pack",
-    "qkv_bias_rope_only": "scalar C restatement",
-    "add_inplace": "scalar C restatement",
+    "qkv_bias_rope_only": "AVX2 vaddps bias, scalar C RoPE-only restatement",
+    "add_inplace": "AVX2 vaddps",
 }
 ROW_KINDS = {"rmsnorm_quantize": 0, "add_rmsnorm_quantize": 1, "kv_pack_f16_kv": 2, "qkv_rope_stage": 3,
              "qkv_bias_rope_only": 4, "add_inplace": 5}  # orc_rows_args.kind (oracle/v7_oracle.h)

@@ -143,6 +143,50 @@ AVX2 void orc_avx2_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, con
 }
 
 /* EVAL_SIGMOID ps, v7_macros.inc:98-160 */
+/* v7s_rmsnorm (src/asm/rmsnorm_kernel.inc:12-75): the order of orc_avx2_fused_add_rmsnorm without the add
+ * (leftover 8-float blocks into A first, then groups of four blocks into A..D; (A+B)+(C+D); HADD_YMM). */
+AVX2 void orc_avx2_rmsnorm(float *o, const float *x, const float *weight, int dim, float eps)
+{
+    ORC_REFERENCE_FP_ENV;
+    int blocks = dim >> 3;
+    __m256 a = _mm256_setzero_ps(), b = _mm256_setzero_ps(), c = _mm256_setzero_ps(), d = _mm256_setzero_ps();
+    const float *r = x;
+    for (int i = 0; i < (blocks & 3); ++i) {
+        __m256 v = _mm256_loadu_ps(r);
+        a = _mm256_fmadd_ps(v, v, a);
+        r += 8;
+    }
+    for (int g = 0; g < (blocks >> 2); ++g) {
+        __m256 x0 = _mm256_loadu_ps(r), x1 = _mm256_loadu_ps(r + 8);
+        __m256 x2 = _mm256_loadu_ps(r + 16), x3 = _mm256_loadu_ps(r + 24);
+        a = _mm256_fmadd_ps(x0, x0, a);
+        b = _mm256_fmadd_ps(x1, x1, b);
+        c = _mm256_fmadd_ps(x2, x2, c);
+        d = _mm256_fmadd_ps(x3, x3, d);
+        r += 32;
+    }
+    a = _mm256_add_ps(a, b);
+    c = _mm256_add_ps(c, d);
+    a = _mm256_add_ps(a, c);
+    __m256 s = _mm256_set1_ps(rms_scale(hadd_ymm(a), dim, eps));
+    for (int i = 0; i < blocks; ++i) {
+        __m256 v = _mm256_mul_ps(s, _mm256_loadu_ps(x + 8 * i));
+        _mm256_storeu_ps(o + 8 * i, _mm256_mul_ps(v, _mm256_loadu_ps(weight + 8 * i)));
+    }
+}
+
+/* v7s_add_inplace (src/asm/add_kernel.inc:26-49) and PQ_BIAS_ADD (src/asm/v7_macros.inc:366-383): x = x + y
+ * with vaddps, 8 floats at a time; the last n % 8 one at a time. */
+AVX2 void orc_avx2_add_inplace(float *x, const float *y, long long n)
+{
+    ORC_REFERENCE_FP_ENV;
+    long long i = 0;
+    for (; i + 8 <= n; i += 8)
+        _mm256_storeu_ps(x + i, _mm256_add_ps(_mm256_loadu_ps(x + i), _mm256_loadu_ps(y + i)));
+    for (; i < n; ++i)
+        x[i] = x[i] + y[i];
+}
+
 static AVX2 __m256 sigmoid_ps(__m256 g)
 {
     const __m256 sign = _mm256_castsi256_ps(_mm256_set1_epi32((int)0x80000000u));

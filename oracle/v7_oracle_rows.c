@@ -10,11 +10,13 @@
  *   QKV_STAGE       Q and K RMSNorm+RoPE, then the K and V rows packed (src/asm/prefill_q8.inc:848-883)
  *   QKV_BIAS_ROPE   PQ_BIAS_ADD over the QKV row, then RoPE only on Q and K (src/asm/v7_macros.inc:366-410)
  *   ADD_INPLACE     v7s_add_inplace (src/asm/add_kernel.inc:26-49)
- * The AVX2 forms of v7_oracle_avx2.c run where one exists (RMSNorm+RoPE, the F16C pack); the others are the
- * scalar restatement of v7_oracle.c.  Nothing here is part of the product. */
+ * The AVX2 forms of v7_oracle_avx2.c run (RMSNorm, RMSNorm+RoPE, the Q8 quantizer, vaddps, the F16C pack),
+ * except RoPE without the norm, which is the scalar restatement of v7_oracle.c.  Nothing here is part of the
+ * product. */
 #define _GNU_SOURCE
 #include <pthread.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <time.h>
 
 #include "v7_oracle.h"
@@ -25,7 +27,7 @@ typedef struct {
     int n_sets, t0, t1, reps;
 } rows_job;
 
-static void rows_run(const orc_rows_args *a, int t0, int t1, int f16c)
+static void rows_run(const orc_rows_args *a, int t0, int t1, int f16c, float *tmp)
 {
     const int dim = a->dim, hd = a->head_dim, nq = a->n_q_heads, nkv = a->n_kv_heads;
     const long long kvd = (long long)nkv * hd;
@@ -34,11 +36,11 @@ static void rows_run(const orc_rows_args *a, int t0, int t1, int f16c)
         float *row = a->qkv ? a->qkv + (long long)t * a->qkv_stride : 0;
         switch (a->kind) {
         case ORC_ROWS_ADD_RMSNORM_Q8:
-            orc_add_inplace(a->x + td, a->add + td, dim);
+            orc_avx2_add_inplace(a->x + td, a->add + td, dim);
             __attribute__((fallthrough));
-        case ORC_ROWS_RMSNORM_Q8:
-            orc_rmsnorm_quantize_rows(a->codes + td, a->scales + (long long)t * (dim / a->gs), a->x + td, a->weight,
-                                      1, dim, a->gs, a->eps);
+        case ORC_ROWS_RMSNORM_Q8: /* the normalised row, then its groups quantized */
+            orc_avx2_rmsnorm(tmp, a->x + td, a->weight, dim, a->eps);
+            orc_avx2_quantize(a->codes + td, tmp, a->scales + (long long)t * (dim / a->gs), dim, a->gs);
             break;
         case ORC_ROWS_QKV_STAGE:
             orc_avx2_rmsnorm_rope_heads(row, nq, hd, a->q_w, a->cos_table, a->sin_table, a->positions[t],
@@ -56,13 +58,13 @@ static void rows_run(const orc_rows_args *a, int t0, int t1, int f16c)
             }
             break;
         case ORC_ROWS_QKV_BIAS_ROPE:
-            orc_bias_add(row, a->bias, (long long)(nq + 2 * nkv) * hd);
+            orc_avx2_add_inplace(row, a->bias, (long long)(nq + 2 * nkv) * hd);
             orc_rope_only_heads(row, nq, hd, a->cos_table, a->sin_table, a->positions[t], a->rope_max_dim);
             orc_rope_only_heads(row + (long long)nq * hd, nkv, hd, a->cos_table, a->sin_table, a->positions[t],
                                 a->rope_max_dim);
             break;
         case ORC_ROWS_ADD_INPLACE:
-            orc_add_inplace(a->x + td, a->add + td, dim);
+            orc_avx2_add_inplace(a->x + td, a->add + td, dim);
             break;
         default:
             break;
@@ -75,8 +77,12 @@ static void *rows_thread(void *p)
     ORC_REFERENCE_FP_ENV;
     rows_job *j = (rows_job *)p;
     const int f16c = orc_f16c_available();
+    float *tmp = (float *)malloc((size_t)(j->sets[0].dim > 0 ? j->sets[0].dim : 1) * sizeof(float));
+    if (!tmp)
+        return 0;
     for (int r = 0; r < j->reps; ++r)
-        rows_run(&j->sets[r % j->n_sets], j->t0, j->t1, f16c);
+        rows_run(&j->sets[r % j->n_sets], j->t0, j->t1, f16c, tmp);
+    free(tmp);
     return 0;
 }
 

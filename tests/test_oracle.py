@@ -19,6 +19,7 @@ tests pin it with facts that do not come from the oracle itself:
 """
 from __future__ import annotations
 
+import ctypes
 import math
 
 import numpy as np
@@ -702,6 +703,19 @@ def test_avx2_matches_scalar_oracle(oracle):
     tq, ts = C.q8_table(9, 100, 512)
     ids = C.rng(10).integers(0, 100, 20).astype(np.int32)
     assert bits_equal(oracle.avx2_embedding_gather(ids, tq, ts, 512), oracle.embedding_gather(ids, tq, ts, 512))
+    # RMSNorm alone (leftover 8-float blocks included) and vaddps, used by the widened rows' timing driver
+    L = oracle.lib()
+    for dim in (8, 40, 256, 4096):
+        xr, wr = C.normal(dim + 2, dim), C.norm_weight(dim + 3, dim)
+        got = np.empty(dim, F)
+        L.orc_avx2_rmsnorm(got.ctypes.data_as(ctypes.c_void_p), xr.ctypes.data_as(ctypes.c_void_p),
+                           wr.ctypes.data_as(ctypes.c_void_p), dim, ctypes.c_float(1e-6))
+        assert bits_equal(got, oracle.rmsnorm(xr[None], wr, 1e-6)[0])
+    xa, ya = C.normal(13, 1003), C.normal(14, 1003)
+    got = xa.copy()
+    L.orc_avx2_add_inplace(got.ctypes.data_as(ctypes.c_void_p), ya.ctypes.data_as(ctypes.c_void_p),
+                           ctypes.c_longlong(1003))
+    assert bits_equal(got, oracle.add_inplace(xa, ya))
 
 
 # --------------------------------------------------------------------------- next rows: rmsnorm, rmsnorm_quantize, add_inplace
