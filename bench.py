@@ -32,7 +32,7 @@ QKV-bias RoPE-only stage, add_inplace), each call timed like the chain's kernels
 the restatement of each row on the host, one call per token row over the host threads, and checks the
 GPU's outputs for the same inputs bit for bit.
 
-    python bench.py [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu] [--no-rows]
 """
 from __future__ import annotations
 
@@ -106,6 +106,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--cpu-tokens", type=int, default=2048)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-rows", action="store_true", help="skip the widened rows (GPU pass and CPU leg)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run one 1 GiB torch copy (the scale reference for rocprofv3 --pmc byte counters)")
     return p.parse_args()
@@ -425,7 +426,7 @@ def cpu_baseline(torch, ops, chain, args):
     # sample (the same rows, still beyond the host caches) for a quarter of the time.
     n1 = max(1, S // 4)
     gbs1, reps1, secs1 = timed(1, n1, args.cpu_seconds / 4)
-    rows = rows_leg(torch, ops, chain, L, cores, max(0.5, args.cpu_seconds / 10))
+    rows = None if args.no_rows else rows_leg(torch, ops, chain, L, cores, max(0.5, args.cpu_seconds / 10))
     ref_so = os.environ.get("V7_REF_SO")
     reference = None
     if ref_so:
@@ -441,7 +442,7 @@ def cpu_baseline(torch, ops, chain, args):
                           "sample": f"{n1} tokens, {reps1} repetitions in {secs1:.1f} s"},
         "cpu_model": cpu_model(),
         "gpu_sample_bit_exact": match,
-        "rows": rows,
+        **({"rows": rows} if rows is not None else {}),
         **({"reference": reference} if reference is not None else {}),
     }
 
@@ -605,10 +606,10 @@ def main():
 
     # The widened rows at the same shapes (after the timed region, not part of `value`): each row's calls
     # timed the same way, alternating two buffer sets.
-    rows = Rows(torch, ops, chain, args.seed)
+    rows_out = None if args.no_rows else {}
+    rows = None if args.no_rows else Rows(torch, ops, chain, args.seed)
     row_reps = max(4, min(args.steps, 20))
-    rows_out = {}
-    for name in ROW_BYTES:
+    for name in (ROW_BYTES if rows is not None else ()):
         for d in rows.sets:
             rows.launch(name, d)
         evr = [(hip.create(), hip.create()) for _ in range(row_reps)]
@@ -660,7 +661,7 @@ def main():
                      "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "us_per_launch": round(dom_ms * 1e3, 2), "algorithmic_bytes": BYTES[DOMINANT]},
         "kernels": kern,
-        "rows": rows_out,
+        **({"rows": rows_out} if rows_out is not None else {}),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
