@@ -80,9 +80,6 @@ struct Lib {
   int (*kv_pack_f16_kv)(uint16_t *, long long, uint16_t *, long long, const float *, const float *, long long, int,
                         int);
   int (*qkv_rope_stage)(const v7g_qkv_stage *);
-  int (*qk_rmsnorm_rope_kv)(float *, long long, int, const float *, float *, long long, int, const float *, int, int,
-                            const float *, const float *, const int32_t *, int, int, int, float, uint16_t *, long long,
-                            int);
   v7s_fused_add_rmsnorm_fn v7s_fused_add_rmsnorm;
   v7s_rmsnorm_rope_heads_fn v7s_rmsnorm_rope_heads;
   v7s_swiglu_quantize_row_fn v7s_swiglu_quantize_row;
@@ -122,7 +119,6 @@ int load(const char *path, Lib &L) {
   resolve(L, L.kv_pack_f16, "v7g_kv_pack_f16");
   resolve(L, L.kv_pack_f16_kv, "v7g_kv_pack_f16_kv");
   resolve(L, L.qkv_rope_stage, "v7g_qkv_rope_stage");
-  resolve(L, L.qk_rmsnorm_rope_kv, "v7g_qk_rmsnorm_rope_kv");
   resolve(L, L.v7s_fused_add_rmsnorm, "v7s_fused_add_rmsnorm");
   resolve(L, L.v7s_rmsnorm_rope_heads, "v7s_rmsnorm_rope_heads");
   resolve(L, L.v7s_swiglu_quantize_row, "v7s_swiglu_quantize_row");
@@ -611,9 +607,10 @@ void run_models(const Lib &L, hipStream_t st, int tokens, const char *only, cons
   }
 }
 
-// Small-batch (decode) steps at the Qwen3-8B shape: per step the embedding gather, add+RMSNorm, Q/K
-// RMSNorm+RoPE with the K cache rows, the V cache rows and SwiGLU -> Q8 for `tokens` tokens.  Eager launches
-// (host time per call and step time), one HIP graph per step replayed, and one graph of all the steps.
+// Small-batch (decode) steps at the Qwen3-8B shape: per step the embedding gather, add+RMSNorm, the Q/K/V
+// stage (Q/K RMSNorm+RoPE, K and V to their binary16 cache rows, one launch) and SwiGLU -> Q8 for `tokens`
+// tokens.  Eager launches (host time per call and step time), one HIP graph per step replayed, and one graph
+// of all the steps.
 void run_decode(const Lib &L, hipStream_t st, int T, const Opts &opt) {
   const int DIM = 4096, VOCAB = 151936, NQ = 32, NKV = 8, HD = 128, HID = 12288, GS = 32, POS = 4096;
   const int N = opt.iterations;
@@ -645,12 +642,23 @@ void run_decode(const Lib &L, hipStream_t st, int T, const Opts &opt) {
   auto step = [&]() {
     bad |= L.embedding_gather_q8(out, ids, T, tq, ts, DIM, VOCAB);
     bad |= L.fused_add_rmsnorm(normed, res, out, w, T, DIM, 1e-6f);
-    bad |= L.qk_rmsnorm_rope_kv(qkv, qs, NQ, qw, qkv + NQ * HD, qs, NKV, kw, T, HD, ct, stb, pos, 0, HD / 2, POS, 1e-6f,
-                                kc, NKV * HD, 0);
-    bad |= L.kv_pack_f16(vc, NKV * HD, qkv + (NQ + NKV) * HD, qs, T, NKV * HD);
+    v7g_qkv_stage g;
+    memset(&g, 0, sizeof(g));
+    g.q = {qkv, qs, NQ, qw, nullptr, nullptr, 0, 1};
+    g.k = {qkv + NQ * HD, qs, NKV, kw, nullptr, kc, (long long)NKV * HD, 0};
+    g.v = {qkv + (NQ + NKV) * HD, qs, NKV, nullptr, nullptr, vc, (long long)NKV * HD, 0};
+    g.n_tokens = T;
+    g.head_dim = HD;
+    g.cos_table = ct;
+    g.sin_table = stb;
+    g.positions = pos;
+    g.rope_max_dim = HD / 2;
+    g.table_rows = POS;
+    g.eps = 1e-6f;
+    bad |= L.qkv_rope_stage(&g);
     bad |= L.swiglu_q8(codes, scales, gate, up, T, HID, GS);
   };
-  constexpr int kCalls = 5;
+  constexpr int kCalls = 4;
   hipEvent_t e0, e1;
   HIPCHECK(hipEventCreate(&e0));
   HIPCHECK(hipEventCreate(&e1));
@@ -688,7 +696,7 @@ void run_decode(const Lib &L, hipStream_t st, int T, const Opts &opt) {
     printf("Fail: a call failed (%d)\n", bad);
     exit(1);
   }
-  printf("Pass: decode step, tokens=%d (5 calls) iterations=%d\n", T, N);
+  printf("Pass: decode step, tokens=%d (%d calls) iterations=%d\n", T, kCalls, N);
   printf("  eager %.2f us / step (host %.2f us / call), graph per step %.2f us, graph of %d steps %.2f us / step\n",
          eager, host_call, g_each, N, g_all);
   printf("{\"kernel\": \"decode_step\", \"tokens\": %d, \"eager_us\": %.3f, \"host_us_per_call\": %.3f, "
