@@ -1,5 +1,6 @@
 """The batched entries and the drop-ins under HIP graph capture: the per-layer chain (Q8 embedding gather, add+RMSNorm,
-Q/K RMSNorm+RoPE inside a fused QKV row, SwiGLU -> Q8) and the RMSNorm -> Q8 / K/V pack rows, captured once
+Q/K RMSNorm+RoPE inside a fused QKV row, SwiGLU -> Q8) and the widened rows (RMSNorm -> Q8, the K/V pack, the Q/K/V
+stage with the QKV bias and both cache rows in the flat layout, add -> RMSNorm -> Q8, add_inplace), captured once
 with torch.cuda.graph on torch's capture stream (the library binds to the caller's current stream) and
 replayed several times, with eager work between the replays (the in-place inputs restored, the outputs
 cleared), each replay checked bit for bit against one eager pass of the same calls; and a one-token decode
@@ -69,6 +70,26 @@ def test_chain_replays_from_a_hip_graph(ops, oracle):
     q = qkv[:, :NQ * HD].view(T, NQ, HD)
     k = qkv[:, NQ * HD:(NQ + NKV) * HD].view(T, NKV, HD)
     v = qkv[:, (NQ + NKV) * HD:]
+    # the Q/K/V stage with the QKV bias and both cache rows over 1030 tokens of 6 + 1 + 1 heads: the flat layout
+    T2, NQ2, NKV2 = 1030, 6, 1
+    qkv2_0 = dev(C.normal(22, (T2, (NQ2 + 2 * NKV2) * HD)))
+    bias2 = dev(C.normal(23, (NQ2 + 2 * NKV2) * HD, 0.5))
+    ct2, st2 = oracle.rope_tables(T2 + 2, HD, 1e6)
+    ct2, st2 = dev(ct2), dev(st2)
+    pos2 = torch.arange(T2, dtype=torch.int32, device="cuda")
+    qkv2 = qkv2_0.clone()
+    kc2 = torch.empty((T2, NKV2, HD), dtype=torch.float16, device="cuda")
+    vc2 = torch.empty((T2, NKV2, HD), dtype=torch.float16, device="cuda")
+    q2 = qkv2[:, :NQ2 * HD].view(T2, NQ2, HD)
+    k2 = qkv2[:, NQ2 * HD:(NQ2 + NKV2) * HD].view(T2, NKV2, HD)
+    v2 = qkv2[:, (NQ2 + NKV2) * HD:].view(T2, NKV2, HD)
+    # add -> RMSNorm -> Q8 (residual updated in place) and add_inplace
+    res3_0 = dev(C.normal(24, (T, DIM)))
+    res3 = res3_0.clone()
+    aq_codes = torch.empty((T, DIM), dtype=torch.int8, device="cuda")
+    aq_scales = torch.empty((T, DIM // 64), device="cuda")
+    xa0 = dev(C.normal(25, (T, DIM)))
+    xa = xa0.clone()
 
     def step():
         ops.embedding_gather_q8(ids, tq, ts, out=emb)
@@ -77,17 +98,29 @@ def test_chain_replays_from_a_hip_graph(ops, oracle):
         ops.swiglu_q8(gate, up, gs=GS, out_q=codes, out_s=scales)
         ops.rmsnorm_quantize(x_nq, w, eps=1e-6, gs=64, out_q=nq_codes, out_s=nq_scales)
         ops.kv_pack_f16_kv(qkv[:, NQ * HD:(NQ + NKV) * HD], v, k_out=kc, v_out=vc)
+        ops.qkv_rope_stage(q2, k2, v2, ct2, st2, positions=pos2, eps=1e-6, q_bias=bias2[:NQ2 * HD],
+                           k_bias=bias2[NQ2 * HD:(NQ2 + NKV2) * HD], v_bias=bias2[(NQ2 + NKV2) * HD:], k_cache=kc2,
+                           v_cache=vc2)
+        ops.add_rmsnorm_quantize(res3, add, w, eps=1e-6, gs=64, out_q=aq_codes, out_s=aq_scales)
+        ops.add_inplace(xa, add)
 
-    outs = (emb, residual, normed, qkv, codes, scales, nq_codes, nq_scales, kc, vc)
+    outs = (emb, residual, normed, qkv, codes, scales, nq_codes, nq_scales, kc, vc, qkv2, kc2, vc2, res3, aq_codes,
+            aq_scales, xa)
+    names = ("emb", "residual", "normed", "qkv", "codes", "scales", "nq codes", "nq scales", "k cache", "v cache",
+             "qkv stage", "qkv stage k cache", "qkv stage v cache", "add+norm->q8 residual", "add+norm->q8 codes",
+             "add+norm->q8 scales", "add_inplace")
 
     def reset():
         residual.copy_(residual0)
         qkv.copy_(qkv0)
-        for o in (emb, normed, scales, nq_scales):
+        qkv2.copy_(qkv2_0)
+        res3.copy_(res3_0)
+        xa.copy_(xa0)
+        for o in (emb, normed, scales, nq_scales, aq_scales):
             o.fill_(-1.0)
-        for o in (codes, nq_codes):
+        for o in (codes, nq_codes, aq_codes):
             o.fill_(0)
-        for o in (kc, vc):
+        for o in (kc, vc, kc2, vc2):
             o.fill_(0)
 
     # one eager pass: the expected outputs
@@ -117,8 +150,7 @@ def test_chain_replays_from_a_hip_graph(ops, oracle):
             torch.cuda.synchronize()
             g.replay()
             torch.cuda.synchronize()
-            for o, w_, name in zip(outs, want, ("emb", "residual", "normed", "qkv", "codes", "scales", "nq codes",
-                                                "nq scales", "k cache", "v cache")):
+            for o, w_, name in zip(outs, want, names):
                 assert np.array_equal(bits(o), w_), (replay, name)
     finally:
         # the library binds each host thread to the stream of its last call: back to the current stream
