@@ -359,6 +359,27 @@ def test_qkv_stage_flat_layout(ops, oracle, T, nq, nkv, hd, norm, bias, keep_k, 
         assert np.isnan(gk[bad]).all()
 
 
+@pytest.mark.parametrize("T,H,hd", [(2050, 3, 64), (2049, 5, 96), (2051, 12, 128), (2053, 3, 256), (1027, 1, 160)])
+def test_single_side_entries_in_the_flat_layout(ops, oracle, T, H, hd):
+    """v7g_rmsnorm_rope_heads and v7g_rope_only_heads over one side whose head count is not a multiple of a
+    wave's heads, from 1024 tokens: the flat layout with a single side (token stride wider than the heads)."""
+    stride = H * hd + 64
+    buf = C.normal(T + H + hd, (T, stride))
+    w = C.norm_weight(hd + 11, hd)
+    ct, st = oracle.rope_tables(T + 1, hd, 1e6 if hd % 64 == 0 else 1e4)
+    pos = C.rng(T + hd).integers(0, T + 1, T).astype(np.int32)
+    pos[[1, T - 1]] = 0
+    heads = buf[:, :H * hd].reshape(T, H, hd)
+    bt = dev(buf)
+    ops.rmsnorm_rope_heads(bt[:, :H * hd].view(T, H, hd), dev(w), dev(ct), dev(st), positions=dev(pos), eps=1e-6)
+    got = host(bt)
+    assert_bits(got[:, :H * hd].reshape(T, H, hd), oracle.rmsnorm_rope(heads, w, ct, st, pos, 1e-6), "rmsnorm_rope")
+    assert_bits(got[:, H * hd:], buf[:, H * hd:], "gap untouched")
+    bt = dev(buf)
+    ops.rope_only_heads(bt[:, :H * hd].view(T, H, hd), dev(ct), dev(st), positions=dev(pos))
+    assert_bits(host(bt)[:, :H * hd].reshape(T, H, hd), oracle.rope_only(heads, ct, st, pos), "rope only")
+
+
 @pytest.mark.parametrize("H", [2, 8])
 def test_rope_position_outside_tables_gives_nan(ops, oracle, H):
     buf = C.normal(9, (3, H, 64))
