@@ -28,9 +28,9 @@ restatement's same two kernels and checked against them bit for bit
 
 `rows` times the widened rows of the path at the same shapes, after the timed region and outside `value`
 (RMSNorm -> Q8, its fused residual-add form, the K/V pack, the Q/K/V stage with binary16 cache rows, the
-QKV-bias RoPE-only stage, add_inplace), each call timed like the chain's kernels; `cpu_baseline.rows` times
-the restatement of each row on the host, one call per token row over the host threads, and checks the
-GPU's outputs for the same inputs bit for bit.
+QKV-bias RoPE-only stage, add_inplace), each row's calls captured in a HIP graph and timed over one replay;
+`cpu_baseline.rows` times the restatement of each row on the host, one call per token row over the host
+threads, and checks the GPU's outputs for the same inputs bit for bit.
 
     python bench.py [--steps K] [--warmup W] [--cpu-seconds S] [--no-cpu] [--no-rows]
 """
@@ -506,7 +506,13 @@ class HipEvents:
         self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
         self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.made = []
+
+    def record(self, e, stream):
+        rc = self.hip.hipEventRecord(e, ctypes.c_void_p(stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
 
     def create(self):
         e = self.ct.c_void_p()
@@ -604,21 +610,35 @@ def main():
             fn()
     torch.cuda.synchronize()
 
-    # The widened rows at the same shapes (after the timed region, not part of `value`): each row's calls
-    # timed the same way, alternating two buffer sets.
+    # The widened rows at the same shapes (after the timed region, not part of `value`): each row's calls,
+    # alternating two buffer sets, captured in a HIP graph and replayed between one pair of events, so that
+    # neither per-call event markers nor the host's time per call (longer than the 18 us K/V pack) sit
+    # between the kernels.
     rows_out = None if args.no_rows else {}
     rows = None if args.no_rows else Rows(torch, ops, chain, args.seed)
     row_reps = max(4, min(args.steps, 20))
     for name in (ROW_BYTES if rows is not None else ()):
         for d in rows.sets:
             rows.launch(name, d)
-        evr = [(hip.create(), hip.create()) for _ in range(row_reps)]
         torch.cuda.synchronize()
-        for i in range(row_reps):
-            lib.v7g_time_next_call(*evr[i])
-            rows.launch(name, rows.sets[i % 2])
+        graph = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.graph(graph):
+                for i in range(row_reps):
+                    rows.launch(name, rows.sets[i % 2])
+        finally:
+            # the library binds each host thread to the stream of its last call: back to the current stream
+            lib.v7g_set_stream(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        graph.replay()
         torch.cuda.synchronize()
-        ms = sum(hip.elapsed_ms(a, b) for a, b in evr) / row_reps
+        e0, e1 = hip.create(), hip.create()
+        stream = torch.cuda.current_stream().cuda_stream
+        hip.record(e0, stream)
+        graph.replay()
+        hip.record(e1, stream)
+        torch.cuda.synchronize()
+        ms = hip.elapsed_ms(e0, e1) / row_reps
+        del graph
         gbs = ROW_BYTES[name] / (ms * 1e-3) / 1e9
         rows_out[name] = {"shape": ROW_SHAPES[name], "bytes": ROW_BYTES[name], "us": round(ms * 1e3, 2),
                           "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
