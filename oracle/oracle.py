@@ -3,8 +3,9 @@
 Only the test suite, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
 ``bench.py`` import this module; the product (``v7multiplikator_amd``) never
 does.  The C restatement lives in ``v7_oracle.c`` (scalar) and
-``v7_oracle_avx2.c`` (AVX2, the CPU baseline); ``make -C oracle`` builds
-``liboracle.so``.
+``v7_oracle_avx2.c`` (AVX2, the CPU baseline); ``v7_oracle_rows.c`` drives
+the widened rows per token row for the baseline's timing; ``make -C oracle``
+builds ``liboracle.so``.
 
 Besides the lane-faithful restatements, this module holds double-precision
 references restating the reference's own C checkers in ``tools/kt_utils.h``
