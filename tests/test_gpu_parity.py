@@ -839,6 +839,40 @@ def test_qkv_stage_cache_only_leaves_f32_k_v(ops, oracle, heads):
     assert_bits(host(vc).view(np.uint16), wvc, "v cache")
 
 
+def test_ops_bind_to_torchs_current_stream(ops):
+    """The torch-facing entries launch on torch's current stream: the raw stream query they use agrees with
+    torch.cuda.current_stream() on the default stream, inside a stream context and under graph capture, where
+    a captured call runs only when the graph replays."""
+    from v7multiplikator_amd import _lib
+    dev = torch.device("cuda", torch.cuda.current_device())
+    assert ops.current_stream_handle(dev) == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert ops.current_stream_handle(dev) == side.cuda_stream
+        x = torch.zeros(4096, device="cuda")
+        ops.add_inplace(x, torch.ones(4096, device="cuda"))
+    side.synchronize()
+    assert bool((x == 1).all())
+    x = torch.zeros(4096, device="cuda")
+    y = torch.full((4096,), 2.0, device="cuda")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    seen = []
+    try:
+        with torch.cuda.graph(g):
+            seen.append((ops.current_stream_handle(dev), torch.cuda.current_stream().cuda_stream))
+            ops.add_inplace(x, y)
+    finally:
+        _lib.load().v7g_set_stream(torch.cuda.current_stream().cuda_stream)
+    assert seen[0][0] == seen[0][1]
+    torch.cuda.synchronize()
+    assert bool((x == 0).all())  # captured, not run
+    g.replay()
+    g.replay()
+    torch.cuda.synchronize()
+    assert bool((x == 4).all())
+
+
 def test_time_next_call_binds_kernel_timestamps(ops):
     """v7g_time_next_call: the armed events time exactly the next launching call, from its kernels'
     own timestamps; a rejected call keeps the pair armed; later calls leave the events alone."""
