@@ -70,9 +70,12 @@ def test_arith_selfcheck_exhaustive(ops):
 
 # --------------------------------------------------------------------------- embedding gather (a9)
 
-# Widths below 8192 that are not multiples of 4096 take one block per row sized to the row; 4096, 8192 and wider
-# rows take 256-thread blocks of 4096 codes (9216: a partial last block).
-@pytest.mark.parametrize("vocab,dim,n", [(1000, 64, 7), (512, 128, 33), (3000, 1024, 100), (4096, 4096, 257),
+# Rows of 256 codes and wider run the flat-piece kernel: groups of 8 workgroups cover 8192 dwords (32768 codes)
+# without a bounds test, a last group with one; a wave's 64 dwords may straddle two rows when dim/4 is not a
+# multiple of 64 (320, 896, 1088, 1152).  Rows below 256 codes take one workgroup per row.
+@pytest.mark.parametrize("vocab,dim,n", [(1000, 64, 7), (512, 128, 33), (1000, 192, 50), (800, 256, 3000),
+                                         (1000, 320, 4099), (700, 896, 1001), (500, 1152, 517), (3000, 1024, 100),
+                                         (4096, 4096, 257), (64, 4096, 1), (64, 4096, 2), (4096, 4096, 64),
                                          (700, 1088, 19), (900, 3072, 41), (600, 2048, 29), (500, 2560, 23),
                                          (400, 3584, 17), (300, 5120, 31), (200, 7168, 9), (300, 8192, 21),
                                          (100, 9216, 13)])
@@ -84,7 +87,7 @@ def test_embedding_gather_matches_oracle(ops, oracle, vocab, dim, n):
     assert_bits(host(got), want, "embedding")
 
 
-@pytest.mark.parametrize("dim", [128, 5120, 9216])
+@pytest.mark.parametrize("dim", [128, 320, 896, 5120, 9216])
 def test_embedding_invalid_ids_give_zero_rows(ops, oracle, dim):
     tq, ts = C.q8_table(3, 64, dim)
     ids = np.array([0, -1, 63, 64, 1 << 30, 5], np.int32)
