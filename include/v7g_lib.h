@@ -180,7 +180,12 @@ V7_ABI void v7s_kv_pack_f16(uint16_t *dest, float *src, int count);
 /* Replaces v7s_rope_init, typedef src/v7_lib.h:275, src/asm/fused_dispatch.inc:58-76:
  * builds the library-owned device cos/sin tables, [131072, head_dim/2] each
  * (positions 0..131071, src/asm/fused_f32_kernel.inc:9), freq_j =
- * base^(-j/(head_dim/2)).  v7g_get_rope_tables returns them. */
+ * base^(-j/(head_dim/2)).  v7g_get_rope_tables returns them.  Like the
+ * reference, which keeps only head_dim and reads the base and the rope type
+ * from the model DB (src/asm/fused_f32_kernel.inc:97-110), it builds from the
+ * configuration set by v7g_set_rope_config when one is set (rope_base is then
+ * ignored; type 1 gives the Llama 3 scaled tables), else plain tables from
+ * rope_base. */
 typedef void(V7_ABI *v7s_rope_init_fn)(int head_dim, float rope_base);
 V7_ABI void v7s_rope_init(int head_dim, float rope_base);
 
@@ -249,6 +254,24 @@ int v7g_build_rope_tables_llama3(float *cos_table, float *sin_table, int n_pos, 
  * model whose rope type is 1); v7g_get_rope_tables returns them. */
 int v7g_rope_init_llama3(int head_dim, float rope_base, int n_pos, float factor, float low_freq_factor,
                          float high_freq_factor, int orig_max_pos);
+/* The model's RoPE configuration for v7s_rope_init, standing in for the model
+ * DB keys the reference's table builder reads (src/asm/fused_f32_kernel.inc:
+ * 49-64,97-110,149-170): rope_type = __sys_rope_type (0 plain, 1 Llama 3),
+ * rope_base = __sys_rope_base, and for type 1 factor, low_freq_factor,
+ * high_freq_factor and orig_max_pos = __sys_rope_factor,
+ * __sys_rope_low_freq_factor, __sys_rope_high_freq_factor and
+ * __sys_rope_orig_max_pos (ignored for type 0).  It plays the role
+ * v7g_set_rms_eps plays for g_rms_eps.  Returns V7G_OK, or V7G_ERR_SHAPE for
+ * another type, a base that is not positive and finite, or Llama 3 parameters
+ * outside factor > 0, 0 < low_freq_factor < high_freq_factor, orig_max_pos > 0
+ * (the configuration is then left as it was).  Process-wide. */
+int v7g_set_rope_config(int rope_type, float rope_base, float factor, float low_freq_factor, float high_freq_factor,
+                        int orig_max_pos);
+/* 1 and the configuration in the non-NULL outputs if one is set, else 0. */
+int v7g_get_rope_config(int *rope_type, float *rope_base, float *factor, float *low_freq_factor,
+                        float *high_freq_factor, int *orig_max_pos);
+/* Forgets the configuration: v7s_rope_init builds plain tables from its argument again. */
+void v7g_clear_rope_config(void);
 
 /* Exhaustive self-check, on the current device, of the arithmetic identities
  * the kernels rely on: mismatches[0] = inputs d in [2^-126, 2^123) where rcp

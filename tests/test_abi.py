@@ -85,6 +85,37 @@ def test_eps_global_roundtrip(L):
         L.v7g_set_rms_eps(old)
 
 
+def test_rope_config_roundtrip_and_rejects(L):
+    """v7g_set_rope_config (the stand-in for the model DB's __sys_rope_* keys that v7s_rope_init reads) keeps
+    what it is given, refuses what the table builder cannot use without touching the stored configuration, and
+    v7g_clear_rope_config forgets it.  No GPU call is made."""
+    c_int, c_f = ctypes.c_int, ctypes.c_float
+    out = [c_int(), c_f(), c_f(), c_f(), c_f(), c_int()]
+    get = lambda: L.v7g_get_rope_config(*(ctypes.byref(v) for v in out))  # noqa: E731
+    L.v7g_clear_rope_config()
+    try:
+        assert get() == 0
+        assert L.v7g_set_rope_config(1, c_f(500000.0), c_f(8.0), c_f(1.0), c_f(4.0), 8192) == 0
+        assert get() == 1
+        assert [v.value for v in out] == [1, 500000.0, 8.0, 1.0, 4.0, 8192]
+        bad = [(2, 1e4, 0, 0, 0, 0), (-1, 1e4, 0, 0, 0, 0), (0, 0.0, 0, 0, 0, 0), (0, -1e4, 0, 0, 0, 0),
+               (0, float("inf"), 0, 0, 0, 0), (0, float("nan"), 0, 0, 0, 0), (1, 1e4, 0.0, 1.0, 4.0, 8192),
+               (1, 1e4, 8.0, 4.0, 4.0, 8192), (1, 1e4, 8.0, 0.0, 4.0, 8192), (1, 1e4, 8.0, 1.0, 4.0, 0)]
+        for t, b, f, lo, hi, op in bad:
+            rc, err = _sticky(L, L.v7g_set_rope_config, t, c_f(b), c_f(f), c_f(lo), c_f(hi), op)
+            assert rc == 2 and err == 2, (t, b, f, lo, hi, op)
+            assert get() == 1 and out[0].value == 1 and out[1].value == 500000.0
+        # type 0 keeps only the base: the Llama 3 fields read back as zero
+        assert L.v7g_set_rope_config(0, c_f(1e6), c_f(8.0), c_f(1.0), c_f(4.0), 8192) == 0
+        assert get() == 1 and [v.value for v in out] == [0, 1e6, 0.0, 0.0, 0.0, 0]
+        assert L.v7g_get_rope_config(None, None, None, None, None, None) == 1
+        L.v7g_clear_rope_config()
+        assert get() == 0
+    finally:
+        L.v7g_clear_rope_config()
+        L.v7g_clear_last_error()
+
+
 def _sticky(L, fn, *args):
     L.v7g_clear_last_error()
     rc = fn(*args)

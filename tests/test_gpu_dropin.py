@@ -168,6 +168,48 @@ def test_v7s_rope_init_tables(shim, oracle):
     assert bits(tc.cpu().numpy(), wc.reshape(-1)) and bits(ts_.cpu().numpy(), ws.reshape(-1))
 
 
+def _owned_tables(L, rows, half):
+    c, s, rmd, npos = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int(), ctypes.c_int()
+    assert L.v7g_get_rope_tables(ctypes.byref(c), ctypes.byref(s), ctypes.byref(rmd), ctypes.byref(npos)) == 0
+    assert rmd.value == half and npos.value == 131072
+    tc = torch.empty(rows * half, dtype=torch.float32, device="cuda")
+    ts_ = torch.empty(rows * half, dtype=torch.float32, device="cuda")
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(tc.data_ptr(), c.value, tc.numel() * 4, 3) == 0  # hipMemcpyDeviceToDevice
+    assert hip.hipMemcpy(ts_.data_ptr(), s.value, ts_.numel() * 4, 3) == 0
+    return tc.cpu().numpy().reshape(rows, half), ts_.cpu().numpy().reshape(rows, half)
+
+
+def test_v7s_rope_init_follows_the_model_config(shim, oracle):
+    """With the model's RoPE configuration set (the stand-in for the DB keys the reference's builder reads,
+    src/asm/fused_f32_kernel.inc:97-110,149-256), an unchanged v7s_rope_init(head_dim, 0.0f) builds the Llama 3
+    scaled tables; a type-0 configuration makes it ignore its float argument; cleared, the argument counts again."""
+    S, L = shim
+    f = ctypes.c_float
+    try:
+        assert L.v7g_set_rope_config(1, f(500000.0), f(8.0), f(1.0), f(4.0), 8192) == 0
+        S.shim_rope_init(128, f(0.0))
+        done(L)
+        wc, ws = oracle.rope_tables_llama3(2048, 128, 500000.0, 8.0, 1.0, 4.0, 8192)
+        gc, gs = _owned_tables(L, 2048, 64)
+        assert bits(gc, wc) and bits(gs, ws)
+        assert L.v7g_set_rope_config(0, f(1e4), f(0.0), f(0.0), f(0.0), 0) == 0
+        S.shim_rope_init(64, f(1e6))  # the argument is ignored: the configured base is 1e4
+        done(L)
+        wc, ws = oracle.rope_tables(1024, 64, 1e4)
+        gc, gs = _owned_tables(L, 1024, 32)
+        assert bits(gc, wc) and bits(gs, ws)
+        L.v7g_clear_rope_config()
+        S.shim_rope_init(64, f(1e6))
+        done(L)
+        wc, ws = oracle.rope_tables(1024, 64, 1e6)
+        gc, gs = _owned_tables(L, 1024, 32)
+        assert bits(gc, wc) and bits(gs, ws)
+    finally:
+        L.v7g_clear_rope_config()
+
+
 @pytest.mark.parametrize("size", [64, 1024, 3072, 8192])
 def test_v7s_rmsnorm_and_rmsnorm_quantize(shim, oracle, size):
     S, L = shim

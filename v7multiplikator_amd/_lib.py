@@ -47,6 +47,9 @@ SIGNATURES = {
     "v7g_build_rope_tables": (_i, [_vp, _vp, _i, _i, _f]),
     "v7g_build_rope_tables_llama3": (_i, [_vp, _vp, _i, _i, _f, _f, _f, _f, _i]),
     "v7g_rope_init_llama3": (_i, [_i, _f, _i, _f, _f, _f, _i]),
+    "v7g_set_rope_config": (_i, [_i, _f, _f, _f, _f, _i]),
+    "v7g_get_rope_config": (_i, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "v7g_clear_rope_config": (None, []),
     "v7g_arith_selfcheck": (_i, [_vp]),
     "v7g_arith_selfcheck_noalloc": (_i, [_vp, _i]),
     "v7g_fused_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),

@@ -36,6 +36,21 @@ float *g_rope_sin = nullptr;
 int g_rope_half = 0;
 int g_rope_npos = 0;
 
+// The model's RoPE configuration, standing in for the model DB keys the
+// reference's table builder reads (__sys_rope_type, __sys_rope_base and, for
+// type 1, __sys_rope_factor, __sys_rope_low_freq_factor,
+// __sys_rope_high_freq_factor, __sys_rope_orig_max_pos;
+// src/asm/fused_f32_kernel.inc:49-64,97-110,149-170).  v7s_rope_init builds
+// from it when it is set and from its own arguments when it is not.
+struct RopeConfig {
+  bool set = false;
+  int type = 0;  // 0 plain, 1 Llama 3 scaled
+  float base = 0.0f, factor = 0.0f, low = 0.0f, high = 0.0f;
+  int orig_max_pos = 0;
+};
+std::mutex g_rope_cfg_mu;
+RopeConfig g_rope_cfg;
+
 constexpr int kRopeMaxPositions = 131072;  // ROPE_INTERNAL_MAX_SEQ_LEN, src/asm/fused_f32_kernel.inc:9
 constexpr int kMaxNormDim = 16384;         // LDS row staging limit of the add+RMSNorm kernel
 
@@ -207,6 +222,9 @@ int check_tables_apart(const float *cos_table, const float *sin_table, int n_pos
   return overlap(v7g::flat_span(cos_table, bytes), v7g::flat_span(sin_table, bytes)) ? V7G_ERR_ALIAS : V7G_OK;
 }
 
+// base^(-j/half) needs a positive finite base (the builder takes its log2).
+int check_rope_base(float base) { return (base > 0.0f && std::isfinite(base)) ? V7G_OK : V7G_ERR_SHAPE; }
+
 int check_llama3(float factor, float low_freq_factor, float high_freq_factor, int orig_max_pos) {
   const bool ok = factor > 0.0f && low_freq_factor > 0.0f && high_freq_factor > low_freq_factor &&
                   orig_max_pos > 0 && std::isfinite(factor) && std::isfinite(high_freq_factor);
@@ -352,6 +370,49 @@ int v7g_rope_init_llama3(int head_dim, float rope_base, int n_pos, float factor,
   const int rc = own_tables(
       n_pos, llama3_freqs(head_dim / 2, rope_base, factor, low_freq_factor, high_freq_factor, orig_max_pos));
   return rc ? fail(rc) : V7G_OK;
+}
+
+int v7g_set_rope_config(int rope_type, float rope_base, float factor, float low_freq_factor, float high_freq_factor,
+                        int orig_max_pos) {
+  if (rope_type != 0 && rope_type != 1) return fail(V7G_ERR_SHAPE);
+  if (int rc = check_rope_base(rope_base)) return fail(rc);
+  if (rope_type == 1)
+    if (int rc = check_llama3(factor, low_freq_factor, high_freq_factor, orig_max_pos)) return fail(rc);
+  RopeConfig c;
+  c.set = true;
+  c.type = rope_type;
+  c.base = rope_base;
+  if (rope_type == 1) {
+    c.factor = factor;
+    c.low = low_freq_factor;
+    c.high = high_freq_factor;
+    c.orig_max_pos = orig_max_pos;
+  }
+  std::lock_guard<std::mutex> lk(g_rope_cfg_mu);
+  g_rope_cfg = c;
+  return V7G_OK;
+}
+
+int v7g_get_rope_config(int *rope_type, float *rope_base, float *factor, float *low_freq_factor,
+                        float *high_freq_factor, int *orig_max_pos) {
+  RopeConfig c;
+  {
+    std::lock_guard<std::mutex> lk(g_rope_cfg_mu);
+    c = g_rope_cfg;
+  }
+  if (!c.set) return 0;
+  if (rope_type) *rope_type = c.type;
+  if (rope_base) *rope_base = c.base;
+  if (factor) *factor = c.factor;
+  if (low_freq_factor) *low_freq_factor = c.low;
+  if (high_freq_factor) *high_freq_factor = c.high;
+  if (orig_max_pos) *orig_max_pos = c.orig_max_pos;
+  return 1;
+}
+
+void v7g_clear_rope_config(void) {
+  std::lock_guard<std::mutex> lk(g_rope_cfg_mu);
+  g_rope_cfg = RopeConfig{};
 }
 
 int v7g_arith_selfcheck(unsigned long long *mismatches) {
@@ -851,6 +912,23 @@ V7_ABI void v7s_swiglu_quantize_row(char *out_q, float *gate, float *up, float *
   v7g_swiglu_q8(reinterpret_cast<int8_t *>(out_q), out_s, gate, up, 1, hidden, 64);
 }
 
-V7_ABI void v7s_rope_init(int head_dim, float rope_base) { v7g_rope_init(head_dim, rope_base, kRopeMaxPositions); }
+// The reference keeps only head_dim from its arguments and reads the base and
+// the rope type from the model DB (src/asm/fused_dispatch.inc:58-76,
+// fused_f32_kernel.inc:97-110): with a configuration set by
+// v7g_set_rope_config the float argument is ignored likewise; without one the
+// tables are plain, from rope_base.
+V7_ABI void v7s_rope_init(int head_dim, float rope_base) {
+  RopeConfig c;
+  {
+    std::lock_guard<std::mutex> lk(g_rope_cfg_mu);
+    c = g_rope_cfg;
+  }
+  if (!c.set)
+    v7g_rope_init(head_dim, rope_base, kRopeMaxPositions);
+  else if (c.type == 1)
+    v7g_rope_init_llama3(head_dim, c.base, kRopeMaxPositions, c.factor, c.low, c.high, c.orig_max_pos);
+  else
+    v7g_rope_init(head_dim, c.base, kRopeMaxPositions);
+}
 
 }  // extern "C"
