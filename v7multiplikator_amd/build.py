@@ -118,22 +118,6 @@ def build_fp_env_probe(verbose: bool = False) -> str:
     return exe
 
 
-def build_stream_probe(verbose: bool = False) -> str:
-    """Measurement: measure/hbm_streams.hip (the HBM ceilings of plain streaming kernels by access mix and by
-    load/store form), built with the library's flags as measure/v7g_hbm_streams.  Not part of libv7g.so and not
-    built by build_library()."""
-    src = os.path.join(PKG, "measure", "hbm_streams.hip")
-    exe = os.path.join(PKG, "measure", "v7g_hbm_streams")
-    cmd = [hipcc(), *[f for f in HIP_FLAGS if f not in ("-shared", "-fPIC")], "-o", exe, src]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in l)
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")
-    return exe
-
-
 def build_test_shim(verbose: bool = False) -> str:
     """Test support: tests/libdropin_shim.so, System V wrappers of the ms_abi drop-in entries."""
     src = os.path.join(ROOT, "tests", "dropin_shim.c")
