@@ -187,14 +187,19 @@ class RowData:
         self.positions = torch.arange(n, dtype=torch.int32, device=device)
 
 
+ROW_SETS = 4  # buffer sets of the widened rows, used in turn
+
+
 class Rows:
-    """Device buffers of the widened rows (two sets, used in turn, so that no call finds its inputs in the
-    Infinity Cache) and one launch per row."""
+    """Device buffers of the widened rows and one launch per row.  ROW_SETS sets are used in turn, so that no
+    call finds its inputs in the 256 MiB Infinity Cache: the smallest row, the K/V pack, touches about 100 MB
+    per call (67 MB of K and V read, 33.5 MB of binary16 rows written), so four sets cycle through about
+    400 MB before a set comes back (two sets, 200 MB, would fit in the cache)."""
 
     def __init__(self, torch, ops, chain, seed):
         self.ops, self.cos, self.sin = ops, chain.cos, chain.sin
         self.sets = []
-        for i in range(2):
+        for i in range(ROW_SETS):
             d = RowData(torch, T, seed + 100 + i, "cuda")
             d.codes = torch.empty((T, DIM), dtype=torch.int8, device="cuda")
             d.scales = torch.empty((T, DIM // 64), dtype=torch.float32, device="cuda")
@@ -611,7 +616,7 @@ def main():
     torch.cuda.synchronize()
 
     # The widened rows at the same shapes (after the timed region, not part of `value`): each row's calls,
-    # alternating two buffer sets, captured in a HIP graph and replayed between one pair of events, so that
+    # rotating through ROW_SETS buffer sets, captured in a HIP graph and replayed between one pair of events, so that
     # neither per-call event markers nor the host's time per call (longer than the 18 us K/V pack) sit
     # between the kernels.
     rows_out = None if args.no_rows else {}
@@ -625,7 +630,7 @@ def main():
         try:
             with torch.cuda.graph(graph):
                 for i in range(row_reps):
-                    rows.launch(name, rows.sets[i % 2])
+                    rows.launch(name, rows.sets[i % len(rows.sets)])
         finally:
             # the library binds each host thread to the stream of its last call: back to the current stream
             lib.v7g_set_stream(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))

@@ -293,8 +293,10 @@ int v7g_arith_selfcheck(unsigned long long *mismatches);
  * written for the selected identities only, with the value
  * v7g_arith_selfcheck gives.  The counts live in 32 bytes of static device
  * memory, one copy per device, kept until the process ends; the entry makes
- * no allocation.  Calls that overlap on one device share those counters and
- * race: serialise them.  Synchronous.  V7G_ERR_SHAPE for checks outside
+ * no allocation.  Every call on a device shares those counters, so a call
+ * holds a per-device lock from clearing them until its counts are read back:
+ * calls from several host threads on one device queue up instead of racing.
+ * Synchronous.  V7G_ERR_SHAPE for checks outside
  * 1..15 (there are four identities, four counters). */
 int v7g_arith_selfcheck_noalloc(unsigned long long *mismatches, int checks);
 

@@ -62,6 +62,7 @@ def lib():
             "orc_add_inplace": (None, [_f32p, _f32p, c_ll]),
             "orc_kv_pack_f16": (None, [_u16p, _f32p, c_ll]),
             "orc_rope_only_heads": (None, [_f32p, c_int, c_int, _f32p, _f32p, c_int, c_int]),
+            "orc_avx2_rope_only_heads": (None, [_f32p, c_int, c_int, _f32p, _f32p, c_int, c_int]),
             "orc_bias_add": (None, [_f32p, _f32p, c_ll]),
             "orc_avx2_kv_pack_f16": (None, [_u16p, _f32p, c_ll]),
             "orc_f16c_available": (c_int, []),

@@ -102,6 +102,8 @@ void orc_avx2_rmsnorm_rope_heads(float *buf, int n_heads, int head_dim, const fl
 void orc_avx2_swiglu(float *out, const float *gate, const float *up, long long n);
 void orc_avx2_rmsnorm(float *o, const float *x, const float *weight, int dim, float eps);
 void orc_avx2_add_inplace(float *x, const float *y, long long n);
+void orc_avx2_rope_only_heads(float *buf, int n_heads, int head_dim, const float *cos_table,
+                              const float *sin_table, int pos, int rope_max_dim);
 void orc_avx2_quantize(int8_t *out_q, const float *in_x, float *out_s, long long n, int gs);
 void orc_avx2_embedding_row(float *out, int token, int dim, const int8_t *table_q, const float *table_s);
 

@@ -187,6 +187,37 @@ AVX2 void orc_avx2_add_inplace(float *x, const float *y, long long n)
         x[i] = x[i] + y[i];
 }
 
+/* RoPE without the norm, v7s_rope_only_head (src/asm/rope_only_kernel.inc:11-53): per 8 pairs
+ * vmulps lo*cos, vmulps lo*sin, vfnmadd231ps (lo*cos - up*sin), vfmadd231ps (lo*sin + up*cos); pos == 0
+ * leaves the heads as they are.  Bit for bit the scalar orc_rope_only_heads (tests/test_oracle.py). */
+AVX2 void orc_avx2_rope_only_heads(float *buf, int n_heads, int head_dim, const float *cos_table,
+                                   const float *sin_table, int pos, int rope_max_dim)
+{
+    ORC_REFERENCE_FP_ENV;
+    if (pos == 0)
+        return;
+    const float *c = cos_table + (long long)pos * rope_max_dim;
+    const float *s = sin_table + (long long)pos * rope_max_dim;
+    const int half = head_dim / 2;
+    for (int h = 0; h < n_heads; ++h) {
+        float *lo = buf + (long long)h * head_dim, *up = lo + half;
+        int j = 0;
+        for (; j + 8 <= half; j += 8) {
+            const __m256 cv = _mm256_loadu_ps(c + j), sv = _mm256_loadu_ps(s + j);
+            const __m256 l = _mm256_loadu_ps(lo + j), u = _mm256_loadu_ps(up + j);
+            const __m256 re = _mm256_fnmadd_ps(u, sv, _mm256_mul_ps(l, cv));
+            const __m256 ro = _mm256_fmadd_ps(u, cv, _mm256_mul_ps(l, sv));
+            _mm256_storeu_ps(lo + j, re);
+            _mm256_storeu_ps(up + j, ro);
+        }
+        for (; j < half; ++j) {
+            const float l = lo[j], u = up[j];
+            lo[j] = fmaf(-u, s[j], l * c[j]);
+            up[j] = fmaf(u, c[j], l * s[j]);
+        }
+    }
+}
+
 static AVX2 __m256 sigmoid_ps(__m256 g)
 {
     const __m256 sign = _mm256_castsi256_ps(_mm256_set1_epi32((int)0x80000000u));

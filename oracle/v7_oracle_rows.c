@@ -10,9 +10,8 @@
  *   QKV_STAGE       Q and K RMSNorm+RoPE, then the K and V rows packed (src/asm/prefill_q8.inc:848-883)
  *   QKV_BIAS_ROPE   PQ_BIAS_ADD over the QKV row, then RoPE only on Q and K (src/asm/v7_macros.inc:366-410)
  *   ADD_INPLACE     v7s_add_inplace (src/asm/add_kernel.inc:26-49)
- * The AVX2 forms of v7_oracle_avx2.c run (RMSNorm, RMSNorm+RoPE, the Q8 quantizer, vaddps, the F16C pack),
- * except RoPE without the norm, which is the scalar restatement of v7_oracle.c.  Nothing here is part of the
- * product. */
+ * The AVX2 forms of v7_oracle_avx2.c run (RMSNorm, RMSNorm+RoPE, RoPE without the norm, the Q8 quantizer,
+ * vaddps, the F16C pack).  Nothing here is part of the product. */
 #define _GNU_SOURCE
 #include <pthread.h>
 #include <stdint.h>
@@ -59,9 +58,9 @@ static void rows_run(const orc_rows_args *a, int t0, int t1, int f16c, float *tm
             break;
         case ORC_ROWS_QKV_BIAS_ROPE:
             orc_avx2_add_inplace(row, a->bias, (long long)(nq + 2 * nkv) * hd);
-            orc_rope_only_heads(row, nq, hd, a->cos_table, a->sin_table, a->positions[t], a->rope_max_dim);
-            orc_rope_only_heads(row + (long long)nq * hd, nkv, hd, a->cos_table, a->sin_table, a->positions[t],
-                                a->rope_max_dim);
+            orc_avx2_rope_only_heads(row, nq, hd, a->cos_table, a->sin_table, a->positions[t], a->rope_max_dim);
+            orc_avx2_rope_only_heads(row + (long long)nq * hd, nkv, hd, a->cos_table, a->sin_table,
+                                     a->positions[t], a->rope_max_dim);
             break;
         case ORC_ROWS_ADD_INPLACE:
             orc_avx2_add_inplace(a->x + td, a->add + td, dim);

@@ -662,6 +662,46 @@ def test_add_rmsnorm_quantize_equals_the_two_calls(ops, oracle, gs, dim):
     assert_bits(host(s), ws, "scales")
 
 
+@pytest.mark.parametrize("gs", [64, 32])
+@pytest.mark.parametrize("rows,dim", [(64, 4096), (2309, 768)])
+@pytest.mark.parametrize("fused_add", [False, True])
+def test_rmsnorm_quantize_codes_4_byte_aligned(ops, oracle, gs, rows, dim, fused_add):
+    """Codes that are 4-byte but not 16-byte aligned (the C ABI accepts them) send dims 512..12288 to the row
+    kernel's 4-elements-per-lane quantizer instead of the 16-per-thread kernel: [64, 4096] runs the 256-thread
+    row, [2309, 768] (more than 2048 rows) the one-wave row.  Through the C ABI, plain and with the fused add,
+    bit-exact against the oracle; the bytes around the codes stay untouched."""
+    import ctypes
+
+    from v7multiplikator_amd import _lib
+    L = _lib.load()
+    x = C.normal(rows + dim + gs, (rows, dim))
+    a = C.normal(rows + dim + gs + 1, (rows, dim))
+    w = C.norm_weight(dim + gs, dim)
+    n = rows * dim
+    qbuf = torch.full((n + 32,), 77, dtype=torch.int8, device="cuda")
+    q_ptr = qbuf.data_ptr() + 4
+    assert q_ptr % 16 == 4
+    st = torch.empty((rows, dim // gs), dtype=torch.float32, device="cuda")
+    xt, at, wt = dev(x), dev(a), dev(w)
+    ops._bind(xt)
+    if fused_add:
+        rc = L.v7g_add_rmsnorm_quantize(q_ptr, st.data_ptr(), xt.data_ptr(), at.data_ptr(), wt.data_ptr(), rows, dim,
+                                        gs, ctypes.c_float(1e-6))
+        x = oracle.add_inplace(x, a)
+    else:
+        rc = L.v7g_rmsnorm_quantize(q_ptr, st.data_ptr(), xt.data_ptr(), wt.data_ptr(), rows, dim, gs,
+                                    ctypes.c_float(1e-6))
+    assert rc == 0
+    torch.cuda.synchronize()
+    wq, ws = oracle.rmsnorm_quantize(x, w, 1e-6, gs)
+    got = host(qbuf)
+    assert_bits(got[4:4 + n].reshape(rows, dim), wq, "codes")
+    assert_bits(host(st), ws, "scales")
+    assert (got[:4] == 77).all() and (got[4 + n:] == 77).all()
+    if fused_add:
+        assert_bits(host(xt), x, "residual")
+
+
 def test_rmsnorm_quantize_config_shape(ops, oracle):
     """The Q8 path's per-token input to QKV/W1/W3 at the Qwen3-8B width: [2048, 4096], GS 64."""
     x = C.normal(11, (2048, 4096))

@@ -716,6 +716,17 @@ def test_avx2_matches_scalar_oracle(oracle):
     L.orc_avx2_add_inplace(got.ctypes.data_as(ctypes.c_void_p), ya.ctypes.data_as(ctypes.c_void_p),
                            ctypes.c_longlong(1003))
     assert bits_equal(got, oracle.add_inplace(xa, ya))
+    # RoPE without the norm (rope_only_kernel.inc's vmulps / vfnmadd231ps / vfmadd231ps order) against the
+    # scalar restatement, at every head_dim class, position 0 (no rotation) and the last table row
+    for hd in (64, 96, 128, 256, 512):
+        ct, st = oracle.rope_tables(40, hd, 1e4)
+        for pos in (0, 1, 17, 39):
+            x = C.normal(hd + pos, (5, hd))
+            want, got = x.copy(), x.copy()
+            L.orc_rope_only_heads(want, 5, hd, ct, st, pos, hd // 2)
+            L.orc_avx2_rope_only_heads(got, 5, hd, ct, st, pos, hd // 2)
+            assert bits_equal(got, want), (hd, pos)
+            assert pos > 0 or bits_equal(got, x)
 
 
 # --------------------------------------------------------------------------- next rows: rmsnorm, rmsnorm_quantize, add_inplace

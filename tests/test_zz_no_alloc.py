@@ -47,6 +47,34 @@ def test_noalloc_selfcheck_equals_the_allocating_entry_twice(L):
     assert list(ref) == [0, 0, 0, 0]  # a conforming device
 
 
+def test_noalloc_selfcheck_from_two_host_threads(L):
+    """Two host threads call the non-allocating entry on the same device at once, twice each: the entry holds
+    a per-device lock from clearing the shared counters until its counts are back, so every call returns the
+    allocating entry's counts for the identities it selects."""
+    import threading
+
+    print("entry: v7g_arith_selfcheck_noalloc(0x3) from two host threads", flush=True)
+    results, errors = [], []
+
+    def worker():
+        try:
+            for _ in range(2):
+                out = _counts([SENTINEL] * 4)
+                rc = L.v7g_arith_selfcheck_noalloc(out, 0x3)
+                results.append((rc, list(out)))
+        except Exception as e:  # noqa: BLE001
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker) for _ in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors and len(results) == 4
+    for rc, out in results:
+        assert rc == 0 and out == [0, 0, SENTINEL, SENTINEL]
+
+
 def test_noalloc_selfcheck_refuses_more_than_four_identities(L):
     out = _counts([SENTINEL] * 4)
     L.v7g_clear_last_error()

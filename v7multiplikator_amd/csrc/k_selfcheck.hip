@@ -167,17 +167,18 @@ int arith_selfcheck(unsigned long long mismatches[4], hipStream_t stream) {
 // is a stand-in, not a device address.  The device address comes from
 // hipGetSymbolAddress, called once per device with that device current, on the
 // entry's first call there.  Every call on a device shares its counters and
-// clears them first: calls that overlap on one device race.
+// clears them first, so a call holds that device's lock from the clear until
+// its counts are back on the host: calls from several host threads on one
+// device run one after another instead of racing on the counters.
 static __device__ __align__(256) unsigned long long scratch[kChecks];
 
 constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static unsigned long long *g_scratch_ptr[kMaxDevices];
+static std::mutex g_device_mu[kMaxDevices];  // one call at a time per device
 
-// The current device's address of `scratch`, or nullptr on a HIP error.
-static unsigned long long *scratch_on_current_device() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+// The address of `scratch` on device dev (current), or nullptr on a HIP error.
+static unsigned long long *scratch_on_device(int dev) {
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void *p = nullptr;
@@ -188,7 +189,10 @@ static unsigned long long *scratch_on_current_device() {
 }
 
 int arith_selfcheck_noalloc(unsigned long long mismatches[4], int checks, hipStream_t stream) {
-  unsigned long long *counters = scratch_on_current_device();
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+  std::lock_guard<std::mutex> call_lock(g_device_mu[dev]);
+  unsigned long long *counters = scratch_on_device(dev);
   if (!counters) return -1;
   enqueue(clear_counters_kernel, dim3(1), dim3(64), 0, stream, counters, kChecks);
   for (int w = 0; w < kChecks; ++w)
