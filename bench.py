@@ -90,7 +90,7 @@ ROW_FORMS = {  # the restatement each row's CPU timing runs (oracle/)
     "add_rmsnorm_quantize": "AVX2 vaddps, RMSNorm and Q8 quantizer restatement",
     "kv_pack_f16_kv": "F16C vcvtps2ph, the reference's instruction",
     "qkv_rope_stage": "AVX2 RMSNorm+RoPE restatement and the F16C pack",
-    "qkv_bias_rope_only": "AVX2 vaddps bias, scalar C RoPE-only restatement",
+    "qkv_bias_rope_only": "AVX2 vaddps bias and RoPE-only restatement (vmulps, vfnmadd231ps, vfmadd231ps)",
     "add_inplace": "AVX2 vaddps",
 }
 ROW_KINDS = {"rmsnorm_quantize": 0, "add_rmsnorm_quantize": 1, "kv_pack_f16_kv": 2, "qkv_rope_stage": 3,
