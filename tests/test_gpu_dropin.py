@@ -114,9 +114,12 @@ def test_v7d_quantize(shim, oracle, n):
     assert bits(qt.cpu().numpy(), wq[0]) and bits(st.cpu().numpy(), ws[0])
 
 
-def test_v7s_embedding_row(shim, oracle):
+@pytest.mark.parametrize("dim", [64, 256, 896, 4096])
+def test_v7s_embedding_row(shim, oracle, dim):
+    """One row per call (no id array: the table is offset to the row): the one-workgroup-per-row kernel below
+    256 codes, the flat-piece kernel's last group of workgroups (its bounds-tested path) from 256 on."""
     S, L = shim
-    vocab, dim = 300, 256
+    vocab = 300
     tq, ts = C.q8_table(31, vocab, dim)
     tqt, tst = dev(tq), dev(ts)
     ids = [0, 7, 299, 150]
