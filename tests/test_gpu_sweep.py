@@ -190,6 +190,26 @@ def test_sweep_embedding_and_kv_pack(ops, oracle):
         assert same(host(hv).view(np.uint16), oracle.kv_pack_f16(qkv[:, q_w + kv:])), ("kv_pack V", n, kv, q_w)
 
 
+def test_sweep_embedding_many_tokens_with_invalid_ids(ops, oracle):
+    """The gather at 1000-5000 tokens (many whole groups of 8 workgroups, then a bounds-tested last group; waves
+    straddling rows wherever dim/4 is not a multiple of 64) with about 2% of the ids outside the table, whose
+    rows must come out as zeros, wherever in a wave or piece they fall."""
+    def draw(r):
+        return int(r.integers(1, 5000)), 64 * int(r.integers(4, 33)), int(r.integers(1000, 5000))
+
+    for vocab, dim, n in shapes("emb_many", draw):
+        tq, ts = C.q8_table(vocab + dim + 1, vocab, dim)
+        r = C.rng(n + vocab + 1)
+        ids = r.integers(0, vocab, n).astype(np.int32)
+        bad = r.random(n) < 0.02
+        ids[bad] = np.where(r.random(int(bad.sum())) < 0.5, -1 - r.integers(0, 1000, int(bad.sum())),
+                            vocab + r.integers(0, 1000, int(bad.sum()))).astype(np.int32)
+        got = host(ops.embedding_gather_q8(dev(ids), dev(tq), dev(ts)))
+        want = np.zeros((n, dim), np.float32)
+        want[~bad] = oracle.embedding_gather(ids[~bad], tq, ts, dim)
+        assert same(got, want), (vocab, dim, n, int(bad.sum()))
+
+
 def test_sweep_qkv_stage(ops, oracle):
     """The Q/K/V stage with three sides: random head counts (partly filled waves), every head_dim class up to
     256, bias or not, norm or RoPE only, binary16 caches with or without the f32 result, random positions
