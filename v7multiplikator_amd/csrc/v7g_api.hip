@@ -771,7 +771,8 @@ int v7g_embedding_gather_q8(float *out, const int32_t *ids, int n_tokens, const 
   if (n_tokens < 0 || dim <= 0 || dim % 64 != 0 || vocab <= 0) return fail(V7G_ERR_SHAPE);
   if (n_tokens == 0) return V7G_OK;
   if (!out || !ids || !table_q || !table_s) return fail(V7G_ERR_NULL);
-  // one 256-thread block per 4096 codes of a row; the grid must stay below 2^32 threads
+  // the one-workgroup-per-row form (rows below 256 codes, launches of 2^32 dwords or more) takes up to
+  // ceil(dim/4096) workgroups per row: its grid stays below 2^24 workgroups
   if ((long long)n_tokens * ((dim / 4 + 1023) / 1024) >= (1LL << 24)) return fail(V7G_ERR_SHAPE);
   if (!al16(out) || ((uintptr_t)table_q & 3u) || ((uintptr_t)table_s & 3u) || ((uintptr_t)ids & 3u))
     return fail(V7G_ERR_ALIGN);
