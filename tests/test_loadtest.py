@@ -15,7 +15,7 @@ PKG = os.path.join(ROOT, "v7multiplikator_amd")
 EXE = os.path.join(PKG, "v7g_loadtest")
 LIB = os.path.join(PKG, "libv7g.so")
 
-MODES = ["fused_add_rmsnorm", "rmsnorm_rope", "swiglu", "swiglu_q8", "embedding", "rmsnorm_quantize",
+MODES = ["fused_add_rmsnorm", "rmsnorm", "add_inplace", "rmsnorm_rope", "swiglu", "swiglu_q8", "embedding", "rmsnorm_quantize",
          "add_rmsnorm_quantize", "kv_pack", "kv_pack_kv", "qkv_stage", "rope_only", "configs", "next", "models",
          "decode"]
 
@@ -42,7 +42,7 @@ def test_usage_names_every_mode(exe):
 @pytest.mark.parametrize("args", [["bogus"], ["fused_add_rmsnorm", "8"], ["rmsnorm_rope", "8", "2", "1"],
                                   ["swiglu_q8", "0", "64"], ["models", "0"], ["models", "Llama-3-8B"],
                                   ["embedding", "8", "-3", "64"], ["fused_add_rmsnorm", "8", "64", "--iterations",
-                                                                   "0"]])
+                                                                   "0"], ["rmsnorm", "8"], ["add_inplace", "0", "64"]])
 def test_bad_arguments_print_usage_before_any_gpu_call(exe, args):
     # the library path does not exist: a run that got past the argument check would report the failed dlopen
     r = run(exe, "/nonexistent/libv7g.so", *args)
@@ -81,13 +81,31 @@ def test_models_mode_runs_the_four_kernels(exe):
                                          (["fused_add_rmsnorm", 64, 5120], "fused_add_rmsnorm"),
                                          (["embedding", 64, 1000, 5120], "embedding_gather_q8"),
                                          (["rmsnorm_quantize", 64, 3584, 64], "rmsnorm_quantize"),
-                                         (["kv_pack_kv", 64, 1024], "kv_pack_f16_kv")])
+                                         (["kv_pack_kv", 64, 1024], "kv_pack_f16_kv"),
+                                         (["rmsnorm", 64, 2048], "rmsnorm"),
+                                         (["add_inplace", 64, 4096], "add_inplace")])
 def test_single_kernel_modes(exe, args, kernel):
     r = run(exe, LIB, *args, "--iterations", 3, "--no-rotate")
     assert r.returncode == 0, r.stdout + r.stderr
     recs = records(r.stdout)
     assert len(recs) == 1 and recs[0]["kernel"] == kernel, recs
     assert recs[0]["us"] > 0 and "cache-resident" in r.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode,bytes_per_call", [("rmsnorm", lambda r, d: 8 * r * d + 4 * d),
+                                                 ("add_inplace", lambda r, d: 12 * r * d)])
+def test_per_row_modes_of_the_adjacent_harnesses(exe, mode, bytes_per_call):
+    """The GPU legs of b_rmsnorm_loadtest and b_add_inplace_loadtest: the batched entry and, with --per-row, the
+    reference-signature entry once per row; both count each tensor once."""
+    rows, dim = 16, 1024
+    for extra in ([], ["--per-row"]):
+        r = run(exe, LIB, mode, rows, dim, "--iterations", 3, "--no-rotate", *extra)
+        assert r.returncode == 0, r.stdout + r.stderr
+        recs = records(r.stdout)
+        assert len(recs) == 1 and recs[0]["kernel"] == mode, recs
+        assert recs[0]["bytes"] == bytes_per_call(rows, dim) and recs[0]["us"] > 0
+        assert ("per-row-calls" in recs[0]["shape"]) == bool(extra)
 
 
 @pytest.mark.gpu

@@ -1,10 +1,13 @@
 // v7g_loadtest.cpp -- GPU leg of the reference's kernel load benchmarks
 // (tools/b_fused_add_rmsnorm_loadtest.cpp, b_rmsnorm_rope_loadtest.cpp,
-// b_swiglu_loadtest.cpp, b_swiglu_q8_loadtest.cpp): times one kernel of
+// b_swiglu_loadtest.cpp, b_swiglu_q8_loadtest.cpp, and the adjacent
+// b_rmsnorm_loadtest.cpp and b_add_inplace_loadtest.cpp): times one kernel of
 // libv7g.so on one GPU and prints the reference's "Pass: ... us / call (GB/s)"
 // lines, plus the fraction of MI355X's 8 TB/s HBM peak.
 //
 //   v7g_loadtest <libv7g.so> fused_add_rmsnorm <rows> <dim>
+//   v7g_loadtest <libv7g.so> rmsnorm <rows> <dim>           (tools/b_rmsnorm_loadtest.cpp)
+//   v7g_loadtest <libv7g.so> add_inplace <rows> <dim>       (tools/b_add_inplace_loadtest.cpp)
 //   v7g_loadtest <libv7g.so> rmsnorm_rope <tokens> <q_heads> <kv_heads> <head_dim>
 //   v7g_loadtest <libv7g.so> swiglu <rows> <hidden>
 //   v7g_loadtest <libv7g.so> swiglu_q8 <rows> <hidden> [gs]
@@ -69,6 +72,8 @@ struct Lib {
   const char *(*error_string)(int);
   int (*build_rope_tables)(float *, float *, int, int, float);
   int (*fused_add_rmsnorm)(float *, float *, const float *, const float *, int, int, float);
+  int (*rmsnorm)(float *, const float *, const float *, int, int, float);
+  int (*add_inplace)(float *, const float *, long long);
   int (*qk_rmsnorm_rope)(float *, long long, int, const float *, float *, long long, int, const float *, int, int,
                          const float *, const float *, const int32_t *, int, int, int, float);
   int (*swiglu_f32)(float *, const float *, const float *, long long);
@@ -81,6 +86,8 @@ struct Lib {
                         int);
   int (*qkv_rope_stage)(const v7g_qkv_stage *);
   v7s_fused_add_rmsnorm_fn v7s_fused_add_rmsnorm;
+  v7s_rmsnorm_fn v7s_rmsnorm;
+  v7s_add_inplace_fn v7s_add_inplace;
   v7s_rmsnorm_rope_heads_fn v7s_rmsnorm_rope_heads;
   v7s_swiglu_quantize_row_fn v7s_swiglu_quantize_row;
   v7s_swiglu_row_fn v7s_swiglu_row;
@@ -110,6 +117,8 @@ int load(const char *path, Lib &L) {
   resolve(L, L.error_string, "v7g_error_string");
   resolve(L, L.build_rope_tables, "v7g_build_rope_tables");
   resolve(L, L.fused_add_rmsnorm, "v7g_fused_add_rmsnorm");
+  resolve(L, L.rmsnorm, "v7g_rmsnorm");
+  resolve(L, L.add_inplace, "v7g_add_inplace");
   resolve(L, L.qk_rmsnorm_rope, "v7g_qk_rmsnorm_rope");
   resolve(L, L.swiglu_f32, "v7g_swiglu_f32");
   resolve(L, L.swiglu_q8, "v7g_swiglu_q8");
@@ -120,6 +129,8 @@ int load(const char *path, Lib &L) {
   resolve(L, L.kv_pack_f16_kv, "v7g_kv_pack_f16_kv");
   resolve(L, L.qkv_rope_stage, "v7g_qkv_rope_stage");
   resolve(L, L.v7s_fused_add_rmsnorm, "v7s_fused_add_rmsnorm");
+  resolve(L, L.v7s_rmsnorm, "v7s_rmsnorm");
+  resolve(L, L.v7s_add_inplace, "v7s_add_inplace");
   resolve(L, L.v7s_rmsnorm_rope_heads, "v7s_rmsnorm_rope_heads");
   resolve(L, L.v7s_swiglu_quantize_row, "v7s_swiglu_quantize_row");
   resolve(L, L.v7s_swiglu_row, "v7s_swiglu_row");
@@ -255,6 +266,70 @@ void run_add_rmsnorm(const Lib &L, hipStream_t st, int rows, int dim, const Opts
     HIPCHECK(hipFree(out[s]));
   }
   HIPCHECK(hipFree(w));
+}
+
+// v7s_rmsnorm over rows of dim floats (the reference's b_rmsnorm_loadtest runs one row of `size`): x read,
+// o written, the weight once.
+void run_rmsnorm(const Lib &L, hipStream_t st, int rows, int dim, const Opts &opt) {
+  const size_t n = (size_t)rows * dim;
+  const double bytes = 2.0 * n * 4 + dim * 4.0;
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(7);
+  std::vector<float *> x(sets), out(sets);
+  for (int s = 0; s < sets; ++s) {
+    x[s] = device_fill<float>(n, r, -1.f, 1.f);
+    out[s] = device_empty<float>(n);
+  }
+  float *w = device_fill<float>(dim, r, 0.5f, 1.5f);
+  int iters = 0;
+  double us;
+  char shape[96];
+  if (opt.per_row) {
+    us = time_calls(L, st, sets, opt, [&](int s) {
+      for (int i = 0; i < rows; ++i) L.v7s_rmsnorm(out[s] + (size_t)i * dim, x[s] + (size_t)i * dim, w, dim);
+    }, &iters);
+    snprintf(shape, sizeof shape, "rows=%d dim=%d per-row-calls", rows, dim);
+  } else {
+    us = time_calls(L, st, sets, opt, [&](int s) { L.rmsnorm(out[s], x[s], w, rows, dim, 1e-6f); }, &iters);
+    snprintf(shape, sizeof shape, "rows=%d dim=%d", rows, dim);
+  }
+  report("rmsnorm", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) {
+    HIPCHECK(hipFree(x[s]));
+    HIPCHECK(hipFree(out[s]));
+  }
+  HIPCHECK(hipFree(w));
+}
+
+// v7s_add_inplace, x += y over rows x dim floats (b_add_inplace_loadtest: one call over n floats): x and y
+// read, x written.  Each call adds y once more to its set's x; the values stay finite over any run here.
+void run_add_inplace(const Lib &L, hipStream_t st, int rows, int dim, const Opts &opt) {
+  const size_t n = (size_t)rows * dim;
+  const double bytes = 3.0 * n * 4;
+  const int sets = sets_for(bytes, opt.rotate);
+  Rng r(8);
+  std::vector<float *> x(sets), y(sets);
+  for (int s = 0; s < sets; ++s) {
+    x[s] = device_fill<float>(n, r, -1.f, 1.f);
+    y[s] = device_fill<float>(n, r, -1e-3f, 1e-3f);
+  }
+  int iters = 0;
+  double us;
+  char shape[96];
+  if (opt.per_row) {
+    us = time_calls(L, st, sets, opt, [&](int s) {
+      for (int i = 0; i < rows; ++i) L.v7s_add_inplace(x[s] + (size_t)i * dim, y[s] + (size_t)i * dim, dim);
+    }, &iters);
+    snprintf(shape, sizeof shape, "rows=%d dim=%d per-row-calls", rows, dim);
+  } else {
+    us = time_calls(L, st, sets, opt, [&](int s) { L.add_inplace(x[s], y[s], (long long)n); }, &iters);
+    snprintf(shape, sizeof shape, "rows=%d dim=%d", rows, dim);
+  }
+  report("add_inplace", shape, iters, us, bytes, sets);
+  for (int s = 0; s < sets; ++s) {
+    HIPCHECK(hipFree(x[s]));
+    HIPCHECK(hipFree(y[s]));
+  }
 }
 
 void run_rope(const Lib &L, hipStream_t st, int T, int nq, int nk, int hd, const Opts &opt) {
@@ -716,7 +791,7 @@ void run_decode(const Lib &L, hipStream_t st, int T, const Opts &opt) {
 }
 
 int usage() {
-  printf("usage: v7g_loadtest <libv7g.so> fused_add_rmsnorm <rows> <dim> | rmsnorm_rope <tokens> <q_heads> "
+  printf("usage: v7g_loadtest <libv7g.so> fused_add_rmsnorm|rmsnorm|add_inplace <rows> <dim> | rmsnorm_rope <tokens> <q_heads> "
          "<kv_heads> <head_dim> | swiglu <rows> <hidden> | swiglu_q8 <rows> <hidden> [gs] | embedding <tokens> "
          "<vocab> <dim> | rmsnorm_quantize|add_rmsnorm_quantize <rows> <dim> [gs] | kv_pack|kv_pack_kv <tokens> <kv_dim> "
          "| qkv_stage <tokens> <q_heads> <kv_heads> <head_dim> | rope_only <tokens> <q_heads> <kv_heads> <head_dim> "
@@ -748,7 +823,7 @@ int main(int argc, char **argv) {
   static const struct {
     const char *mode;
     size_t min_args;  // positional arguments including the mode
-  } kModes[] = {{"fused_add_rmsnorm", 3}, {"rmsnorm_rope", 5}, {"swiglu", 3}, {"swiglu_q8", 3}, {"embedding", 4},
+  } kModes[] = {{"fused_add_rmsnorm", 3}, {"rmsnorm", 3}, {"add_inplace", 3}, {"rmsnorm_rope", 5}, {"swiglu", 3}, {"swiglu_q8", 3}, {"embedding", 4},
                 {"rmsnorm_quantize", 3}, {"add_rmsnorm_quantize", 3}, {"kv_pack", 3}, {"kv_pack_kv", 3},
                 {"qkv_stage", 5}, {"rope_only", 5}, {"models", 1}, {"next", 1}, {"configs", 1}, {"decode", 1}};
   bool known = false;
@@ -789,6 +864,10 @@ int main(int argc, char **argv) {
   const std::string k = pos[0];
   if (k == "fused_add_rmsnorm" && pos.size() >= 3)
     run_add_rmsnorm(L, st, num(1, 0), num(2, 0), opt);
+  else if (k == "rmsnorm" && pos.size() >= 3)
+    run_rmsnorm(L, st, num(1, 0), num(2, 0), opt);
+  else if (k == "add_inplace" && pos.size() >= 3)
+    run_add_inplace(L, st, num(1, 0), num(2, 0), opt);
   else if (k == "rmsnorm_rope" && pos.size() >= 5)
     run_rope(L, st, num(1, 0), num(2, 0), num(3, 0), num(4, 0), opt);
   else if (k == "swiglu" && pos.size() >= 3)
@@ -823,6 +902,8 @@ int main(int argc, char **argv) {
     run_kv_pack(L, st, 8192, 1024, false, opt);
     run_kv_pack(L, st, 8192, 1024, true, opt);
     run_qkv_stage(L, st, 8192, 32, 8, 128, opt);
+    run_rmsnorm(L, st, 8192, 4096, opt);
+    run_add_inplace(L, st, 8192, 4096, opt);
   } else if (k == "configs") {
     // The benchmark configurations: C1 .. C4, then the four kernels of the
     // Qwen3-8B T=8192 per-layer chain (C5a .. C5d).
