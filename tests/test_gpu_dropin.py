@@ -231,7 +231,7 @@ def test_v7s_rmsnorm_and_rmsnorm_quantize(shim, oracle, size):
     assert bits(qt.cpu().numpy(), wq[0]) and bits(st.cpu().numpy(), ws[0])
 
 
-@pytest.mark.parametrize("n", [32, 96, 160, 2048, 2051])
+@pytest.mark.parametrize("n", [32, 64, 96, 128, 160, 1024, 2048, 2051])  # tools/v_add_inplace_validate.cpp's sizes
 def test_v7s_add_inplace(shim, oracle, n):
     S, L = shim
     x = C.validator_row(n, n)
