@@ -267,6 +267,29 @@ def test_ops_refuse_host_tensors():
         ops.quantize_q8(x.double())
 
 
+def test_stream_query_falls_back_to_the_public_call(monkeypatch):
+    """A raw current-stream query that rejects its argument hands over to torch.cuda.current_stream for good."""
+    torch = pytest.importorskip("torch")
+    from v7multiplikator_amd import ops
+
+    calls = []
+
+    def raw(index):
+        calls.append(index)
+        raise TypeError("signature changed")
+
+    class Public:
+        cuda_stream = 0x5000
+
+    monkeypatch.setattr(ops, "_raw_stream", raw)
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: Public())
+    dev = torch.device("cuda", 0)
+    assert ops.current_stream_handle(dev) == 0x5000
+    assert ops._raw_stream is None
+    assert ops.current_stream_handle(dev) == 0x5000
+    assert calls == [0]
+
+
 def test_stream_binding_is_per_host_thread(L):
     """v7g_set_stream binds the calling thread's launch stream; another thread keeps its own."""
     import threading

@@ -42,9 +42,14 @@ _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def current_stream_handle(device: torch.device) -> int:
-    """The hipStream_t of torch's current stream on `device`."""
+    """The hipStream_t of torch's current stream on `device`.  If the raw query rejects its argument (a torch
+    that changed its signature), the public call takes over for the rest of the process."""
+    global _raw_stream
     if _raw_stream is not None:
-        return _raw_stream(device.index)
+        try:
+            return _raw_stream(device.index)
+        except (TypeError, RuntimeError):
+            _raw_stream = None
     return torch.cuda.current_stream(device).cuda_stream
 
 
