@@ -187,3 +187,78 @@ def test_embedding_gather_on_both_sides_of_the_32_bit_dword_limit(ops):
         want = np.zeros((len(pick), dim), np.float32)
         want[valid] = table[sel[valid]]
         assert same(got, want), n
+
+
+def test_quantize_q8_generic_rows_past_2_pow_32_elements(ops, oracle):
+    """Q8 quantize (GS 64) of rows of 4100 floats (the general kernel: one thread per group, a 4-element tail
+    group per row) over 1,047,553 rows = 4,294,967,300 elements; sampled rows against the oracle."""
+    rows, row_len = 1047553, 4100
+    need(4 * rows * row_len + rows * row_len + rows * 65 * 4)
+    g = gen(912)
+    x = torch.empty((rows, row_len), dtype=torch.float32, device="cuda").normal_(generator=g)
+    q, s = ops.quantize_q8(x, gs=64)
+    pick = sample_rows(rows, row_len)
+    wq, ws = oracle.quantize(host_rows(x, pick), 64)
+    assert same(host_rows(q, pick), wq) and same(host_rows(s, pick), ws)
+
+
+def test_rmsnorm_past_2_pow_32_elements(ops, oracle):
+    """out = RMSNorm(x) * w over [1048577, 4096]; sampled rows against the oracle."""
+    rows, dim = (1 << 20) + 1, 4096
+    need(2 * 4 * rows * dim)
+    g = gen(913)
+    x = torch.empty((rows, dim), dtype=torch.float32, device="cuda").normal_(generator=g)
+    w = torch.from_numpy(C.norm_weight(914, dim)).cuda()
+    o = ops.rmsnorm(x, w, eps=1e-6)
+    pick = sample_rows(rows, dim)
+    assert same(host_rows(o, pick), oracle.rmsnorm(host_rows(x, pick), w.cpu().numpy(), 1e-6))
+
+
+def test_kv_pack_past_2_pow_32_elements(ops, oracle):
+    """binary16 packing of [2097153, 2048] f32 rows (4.3e9 floats): the whole rows with one launch, then their
+    K and V halves as the two sides of the one-launch pack; sampled rows against the oracle."""
+    rows, width = 2097153, 2048
+    need(4 * rows * width + 2 * rows * width)
+    g = gen(915)
+    src = torch.empty((rows, width), dtype=torch.float32, device="cuda").normal_(generator=g)
+    pick = sample_rows(rows, width)
+    src_rows = host_rows(src, pick)
+    out = ops.kv_pack_f16(src)
+    assert same(host_rows(out, pick).view(np.uint16), oracle.kv_pack_f16(src_rows))
+    del out
+    half = width // 2
+    hk, hv = ops.kv_pack_f16_kv(src[:, :half], src[:, half:])
+    assert same(host_rows(hk, pick).view(np.uint16), oracle.kv_pack_f16(src_rows[:, :half]))
+    assert same(host_rows(hv, pick).view(np.uint16), oracle.kv_pack_f16(src_rows[:, half:]))
+
+
+def test_qkv_stage_with_caches_past_2_pow_32_elements(ops, oracle):
+    """The Q/K/V stage with a QKV bias, RoPE only (no norm weights) and binary16 K/V cache rows, in place
+    inside 700,000 fused QKV rows of 6144 floats (4.3e9 floats; 32 + 8 + 8 heads of 128); sampled tokens
+    against the oracle."""
+    n, nq, nkv, hd = 700000, 32, 8, 128
+    width = (nq + 2 * nkv) * hd
+    need(4 * n * width + 2 * 2 * n * nkv * hd)
+    g = gen(916)
+    qkv = torch.empty((n, width), dtype=torch.float32, device="cuda").normal_(generator=g)
+    qb, kb, vb = (C.normal(917 + i, (h * hd,), 0.5) for i, h in enumerate((nq, nkv, nkv)))
+    ct, st = oracle.rope_tables(8192, hd, 1e6)
+    pos = (np.arange(n, dtype=np.int64) * 7 % 8192).astype(np.int32)
+    pick = sample_rows(n, width)
+    before = host_rows(qkv, pick)
+    kc = torch.empty((n, nkv, hd), dtype=torch.float16, device="cuda")
+    vc = torch.empty((n, nkv, hd), dtype=torch.float16, device="cuda")
+    k0, v0 = nq * hd, (nq + nkv) * hd
+    ops.qkv_rope_stage(qkv[:, :k0].view(n, nq, hd), qkv[:, k0:v0].view(n, nkv, hd), qkv[:, v0:].view(n, nkv, hd),
+                       torch.from_numpy(ct).cuda(), torch.from_numpy(st).cuda(), positions=torch.from_numpy(pos).cuda(),
+                       q_bias=torch.from_numpy(qb).cuda(), k_bias=torch.from_numpy(kb).cuda(),
+                       v_bias=torch.from_numpy(vb).cuda(), k_cache=kc, v_cache=vc)
+    after = host_rows(qkv, pick)
+    wq, wk, wv, wkc, wvc = oracle.qkv_stage(before[:, :k0].reshape(-1, nq, hd), before[:, k0:v0].reshape(-1, nkv, hd),
+                                            before[:, v0:].reshape(-1, nkv, hd), None, None, qb, kb, vb, ct, st,
+                                            pos[pick], 1e-6)
+    assert same(after[:, :k0].reshape(-1, nq, hd), wq)
+    assert same(after[:, k0:v0].reshape(-1, nkv, hd), wk)
+    assert same(after[:, v0:].reshape(-1, nkv, hd), wv)
+    assert same(host_rows(kc, pick).view(np.uint16), wkc)
+    assert same(host_rows(vc, pick).view(np.uint16), wvc)
