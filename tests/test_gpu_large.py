@@ -262,3 +262,20 @@ def test_qkv_stage_with_caches_past_2_pow_32_elements(ops, oracle):
     assert same(after[:, v0:].reshape(-1, nkv, hd), wv)
     assert same(host_rows(kc, pick).view(np.uint16), wkc)
     assert same(host_rows(vc, pick).view(np.uint16), wvc)
+
+
+def test_kv_pack_kv_with_a_row_stride_past_2_pow_32(ops, oracle):
+    """The one-launch K/V pack with a source row stride of 2^32 + 4096 floats (two rows 17.2 GB apart): the
+    kernel form with 64-bit strides, which the launcher takes when a stride does not fit 32 bits."""
+    stride = (1 << 32) + 4096
+    need(4 * (stride + 2048))
+    g = gen(920)
+    flat = torch.empty(stride + 2048, dtype=torch.float32, device="cuda")
+    flat[:2048].normal_(generator=g)
+    flat[stride:].normal_(generator=g)
+    k_src = flat.as_strided((2, 1024), (stride, 1))
+    v_src = flat.as_strided((2, 1024), (stride, 1), 1024)
+    hk, hv = ops.kv_pack_f16_kv(k_src, v_src)
+    rows = np.stack([flat[:2048].cpu().numpy(), flat[stride:].cpu().numpy()])
+    assert same(hk.cpu().numpy().view(np.uint16), oracle.kv_pack_f16(rows[:, :1024]))
+    assert same(hv.cpu().numpy().view(np.uint16), oracle.kv_pack_f16(rows[:, 1024:]))

@@ -61,6 +61,45 @@ struct RopeArgs {
   float eps;
 };
 
+// The fields a wave reads before its first load also travel ahead of the
+// argument block as scalar kernel arguments (14 dwords): the firmware
+// preloads the first 14 argument dwords into SGPRs at wave launch, where a
+// field of the by-value block is fetched with a scalar load and waited for
+// (about 0.4 us of every launch at 32 + 8 heads of 128, from 1024 to 16384
+// tokens).  The kernel rebuilds the block with them (RopeArgs a =
+// V7G_ROPE_ARGS); enqueue_rope passes them.
+#define V7G_ROPE_HOT                                                                                             \
+  unsigned hot_n_waves, int hot_waves_per_token, int hot_wave0, int hot_wave01, const int32_t *hot_positions, \
+      const float *hot_cos, const float *hot_sin, int hot_rope_max_dim, int hot_table_rows, int hot_pos0,    \
+      int hot_head_dim, RopeArgs a_in
+#define V7G_ROPE_ARGS                                                                                        \
+  with_hot(a_in, hot_n_waves, hot_waves_per_token, hot_wave0, hot_wave01, hot_positions, hot_cos, hot_sin, \
+           hot_rope_max_dim, hot_table_rows, hot_pos0, hot_head_dim)
+
+__device__ __forceinline__ RopeArgs with_hot(RopeArgs a, unsigned n_waves, int waves_per_token, int wave0, int wave01,
+                                             const int32_t *positions, const float *cos_table,
+                                             const float *sin_table, int rope_max_dim, int table_rows, int pos0,
+                                             int head_dim) {
+  a.n_waves = n_waves;
+  a.waves_per_token = waves_per_token;
+  a.wave0 = wave0;
+  a.wave01 = wave01;
+  a.positions = positions;
+  a.cos_table = cos_table;
+  a.sin_table = sin_table;
+  a.rope_max_dim = rope_max_dim;
+  a.table_rows = table_rows;
+  a.pos0 = pos0;
+  a.head_dim = head_dim;
+  return a;
+}
+
+template <typename... KArgs>
+static void enqueue_rope(void (*kernel)(KArgs...), dim3 grid, hipStream_t stream, const RopeArgs &a) {
+  enqueue(kernel, grid, dim3(256), 0, stream, a.n_waves, a.waves_per_token, a.wave0, a.wave01, a.positions,
+          a.cos_table, a.sin_table, a.rope_max_dim, a.table_rows, a.pos0, a.head_dim, a);
+}
+
 // Where head f (flat over tokens x heads of all sides) lives, and what to do with it.
 struct HeadRef {
   float *x;        // this lane's first float of the head
@@ -288,7 +327,8 @@ __device__ float kZeroRow[256] = {};  // never written; not const, so it stays i
 // kernel measured about 1 us faster on the Q/K/V stage than one with the bias
 // code taken out.
 template <int K, bool BW>
-__global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rmsnorm_rope_wave_kernel(RopeArgs a) {
+__global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rmsnorm_rope_wave_kernel(V7G_ROPE_HOT) {
+  const RopeArgs a = V7G_ROPE_ARGS;
   static_assert(K >= 2 && K <= 7, "head_dim 64 to 224 (256: rmsnorm_rope_wave16_kernel)");
   constexpr bool ODD = K % 2 == 1;
   constexpr int KH = K / 2;         // even K: the partner of block k is block k + KH in the same lane
@@ -440,7 +480,8 @@ __device__ __forceinline__ float ror8_f(float v) {  // lane l gets lane l ^ 8 of
 // layout of the 8-lane kernel below; the position, the table rows, the
 // out-of-table NaN and the rotation are then per 16-lane group.
 template <bool BW, bool FLAT = false>
-__global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave16_kernel(RopeArgs a) {
+__global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave16_kernel(V7G_ROPE_HOT) {
+  const RopeArgs a = V7G_ROPE_ARGS;
   constexpr int HD = 256;
   const int m = threadIdx.x & 7;
   const int h = (threadIdx.x >> 3) & 1;
@@ -584,7 +625,8 @@ __global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave16_kernel(RopeArgs a)
 // for every lane; a head's 8 lanes share one token).  Arithmetic, order and
 // bias handling (BW) are rmsnorm_rope_wave_kernel's.
 template <int K, bool BW>
-__global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rmsnorm_rope_flat_kernel(RopeArgs a) {
+__global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rmsnorm_rope_flat_kernel(V7G_ROPE_HOT) {
+  const RopeArgs a = V7G_ROPE_ARGS;
   static_assert(K >= 2 && K <= 7, "head_dim 64 to 224");
   constexpr bool ODD = K % 2 == 1;
   constexpr int KH = K / 2;
@@ -729,9 +771,9 @@ static void launch_k(const RopeArgs &a, bool flat, hipStream_t stream) {
       }
       const dim3 grid((a.n_waves + 3u) / 4u);
       if (any_bias && !norm_and_bias)
-        enqueue((rmsnorm_rope_flat_kernel<K, true>), grid, dim3(256), 0, stream, a);
+        enqueue_rope((rmsnorm_rope_flat_kernel<K, true>), grid, stream, a);
       else
-        enqueue((rmsnorm_rope_flat_kernel<K, false>), grid, dim3(256), 0, stream, a);
+        enqueue_rope((rmsnorm_rope_flat_kernel<K, false>), grid, stream, a);
       return;
     }
   }
@@ -747,16 +789,16 @@ static void launch_k(const RopeArgs &a, bool flat, hipStream_t stream) {
       const dim3 grid((a.n_waves + 3u) / 4u);
       if constexpr (K == 8) {  // head_dim 256: 4 heads per wave (the host's wave layout)
         if (flat)
-          bw ? enqueue((rmsnorm_rope_wave16_kernel<true, true>), grid, dim3(256), 0, stream, a)
-             : enqueue((rmsnorm_rope_wave16_kernel<false, true>), grid, dim3(256), 0, stream, a);
+          bw ? enqueue_rope((rmsnorm_rope_wave16_kernel<true, true>), grid, stream, a)
+             : enqueue_rope((rmsnorm_rope_wave16_kernel<false, true>), grid, stream, a);
         else if (bw)
-          enqueue((rmsnorm_rope_wave16_kernel<true>), grid, dim3(256), 0, stream, a);
+          enqueue_rope((rmsnorm_rope_wave16_kernel<true>), grid, stream, a);
         else
-          enqueue((rmsnorm_rope_wave16_kernel<false>), grid, dim3(256), 0, stream, a);
+          enqueue_rope((rmsnorm_rope_wave16_kernel<false>), grid, stream, a);
       } else if (bw) {
-        enqueue((rmsnorm_rope_wave_kernel<K, true>), grid, dim3(256), 0, stream, a);
+        enqueue_rope((rmsnorm_rope_wave_kernel<K, true>), grid, stream, a);
       } else {
-        enqueue((rmsnorm_rope_wave_kernel<K, false>), grid, dim3(256), 0, stream, a);
+        enqueue_rope((rmsnorm_rope_wave_kernel<K, false>), grid, stream, a);
       }
       return;
     }
