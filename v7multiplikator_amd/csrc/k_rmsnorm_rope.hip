@@ -45,6 +45,7 @@ struct RopeArgs {
   int n_heads0, n_heads01;  // side 0 heads; sides 0 + 1 heads
   int heads_per_token;      // heads of all sides
   unsigned n_heads;         // n_tokens * heads_per_token
+  unsigned n_tokens;
   // The wave kernels' grid: per token, ceil(heads / 8) waves for each side (heads / 4 at head_dim 256);
   // the flat layout's: per group of 8 tokens (4 at head_dim 256), heads waves for each side
   // (waves_per_token then counts a group).
@@ -61,7 +62,8 @@ struct RopeArgs {
   float eps;
 };
 
-// The fields a wave reads before its first load also travel ahead of the
+// The fields a wave reads before its first load (its wave index fields,
+// the token count, the positions and the tables) also travel ahead of the
 // argument block as scalar kernel arguments (14 dwords): the firmware
 // preloads the first 14 argument dwords into SGPRs at wave launch, where a
 // field of the by-value block is fetched with a scalar load and waited for
@@ -71,15 +73,15 @@ struct RopeArgs {
 #define V7G_ROPE_HOT                                                                                             \
   unsigned hot_n_waves, int hot_waves_per_token, int hot_wave0, int hot_wave01, const int32_t *hot_positions, \
       const float *hot_cos, const float *hot_sin, int hot_rope_max_dim, int hot_table_rows, int hot_pos0,    \
-      int hot_head_dim, RopeArgs a_in
+      unsigned hot_n_tokens, RopeArgs a_in
 #define V7G_ROPE_ARGS                                                                                        \
   with_hot(a_in, hot_n_waves, hot_waves_per_token, hot_wave0, hot_wave01, hot_positions, hot_cos, hot_sin, \
-           hot_rope_max_dim, hot_table_rows, hot_pos0, hot_head_dim)
+           hot_rope_max_dim, hot_table_rows, hot_pos0, hot_n_tokens)
 
 __device__ __forceinline__ RopeArgs with_hot(RopeArgs a, unsigned n_waves, int waves_per_token, int wave0, int wave01,
                                              const int32_t *positions, const float *cos_table,
                                              const float *sin_table, int rope_max_dim, int table_rows, int pos0,
-                                             int head_dim) {
+                                             unsigned n_tokens) {
   a.n_waves = n_waves;
   a.waves_per_token = waves_per_token;
   a.wave0 = wave0;
@@ -90,14 +92,14 @@ __device__ __forceinline__ RopeArgs with_hot(RopeArgs a, unsigned n_waves, int w
   a.rope_max_dim = rope_max_dim;
   a.table_rows = table_rows;
   a.pos0 = pos0;
-  a.head_dim = head_dim;
+  a.n_tokens = n_tokens;
   return a;
 }
 
 template <typename... KArgs>
 static void enqueue_rope(void (*kernel)(KArgs...), dim3 grid, hipStream_t stream, const RopeArgs &a) {
   enqueue(kernel, grid, dim3(256), 0, stream, a.n_waves, a.waves_per_token, a.wave0, a.wave01, a.positions,
-          a.cos_table, a.sin_table, a.rope_max_dim, a.table_rows, a.pos0, a.head_dim, a);
+          a.cos_table, a.sin_table, a.rope_max_dim, a.table_rows, a.pos0, a.n_tokens, a);
 }
 
 // Where head f (flat over tokens x heads of all sides) lives, and what to do with it.
@@ -342,13 +344,16 @@ __global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rms
   const unsigned t = wvv / (unsigned)a.waves_per_token;
   const int r = (int)(wvv - t * (unsigned)a.waves_per_token);
   const int sd = r < a.wave0 ? 0 : (r < a.wave01 ? 1 : 2);
-  const RopeSide &S = a.side[sd];
+  const RopeSide S = a.side[sd];  // a copy: every field is requested before the barrier below
   const int hs_raw = 8 * (r - (sd == 0 ? 0 : (sd == 1 ? a.wave0 : a.wave01))) + ((threadIdx.x & 63) >> 3);
   const bool live = live_wave && hs_raw < S.n_heads;
   const int hs = hs_raw < S.n_heads ? hs_raw : S.n_heads - 1;
-  const size_t in_head = (size_t)hs * a.head_dim + 4 * m;
+  const size_t in_head = (size_t)hs * (32 * K) + 4 * m;
   float *x = S.buf + (size_t)t * (size_t)S.token_stride + in_head;
   int pos = a.positions ? a.positions[t] : a.pos0 + (int)t;
+  // The side's fields and the position are requested together, in one round
+  // of scalar loads, before the head's loads are addressed.
+  asm volatile("" ::: "memory");
   // A position outside the tables cannot be read: its rotated heads become NaN.
   const bool bad_pos = S.rotate && pos != 0 && (unsigned)pos >= (unsigned)a.table_rows;
   if (bad_pos) pos = 0;
@@ -492,13 +497,14 @@ __global__ __launch_bounds__(256, 8) void rmsnorm_rope_wave16_kernel(V7G_ROPE_HO
   const unsigned grp = wvv / (unsigned)a.waves_per_token;  // the token, or with FLAT the group of 4 tokens
   const int r = (int)(wvv - grp * (unsigned)a.waves_per_token);
   const int sd = r < a.wave0 ? 0 : (r < a.wave01 ? 1 : 2);
-  const RopeSide &S = a.side[sd];
+  const RopeSide S = a.side[sd];  // a copy: every field is requested here, in one round
+  asm volatile("" ::: "memory");
   const int hs_raw = 4 * (r - (sd == 0 ? 0 : (sd == 1 ? a.wave0 : a.wave01))) + ((threadIdx.x & 63) >> 4);
   bool live;
   int hs;
   unsigned t;
   if constexpr (FLAT) {  // hs_raw is the pair's index among the side's 4 * n_heads pairs of the group
-    const unsigned n_tokens = a.n_heads / (unsigned)a.heads_per_token;
+    const unsigned n_tokens = a.n_tokens;
     const unsigned tl = (unsigned)hs_raw / (unsigned)S.n_heads;
     hs = hs_raw - (int)(tl * (unsigned)S.n_heads);
     const unsigned tg = 4u * grp + tl;
@@ -640,8 +646,9 @@ __global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rms
   const unsigned grp = wvv / (unsigned)a.waves_per_token;  // waves_per_token: waves per group of 8 tokens
   const int r = (int)(wvv - grp * (unsigned)a.waves_per_token);
   const int sd = r < a.wave0 ? 0 : (r < a.wave01 ? 1 : 2);
-  const RopeSide &S = a.side[sd];
-  const unsigned n_tokens = a.n_heads / (unsigned)a.heads_per_token;
+  const RopeSide S = a.side[sd];  // a copy: every field is requested here, in one round
+  asm volatile("" ::: "memory");
+  const unsigned n_tokens = a.n_tokens;
   const unsigned nh = (unsigned)S.n_heads;
   const unsigned pair = 8u * (unsigned)(r - (sd == 0 ? 0 : (sd == 1 ? a.wave0 : a.wave01))) +
                         ((threadIdx.x & 63u) >> 3);
@@ -652,7 +659,7 @@ __global__ __launch_bounds__(256, (K == 2 || K == 3 || K == 4) ? 8 : 1) void rms
   const unsigned tt = t < n_tokens ? t : n_tokens - 1;
   int pos = a.positions ? a.positions[tt] : a.pos0 + (int)tt;
   asm volatile("" ::: "memory");  // the position's load goes out ahead of the head's
-  const size_t in_head = (size_t)h * a.head_dim + 4 * m;
+  const size_t in_head = (size_t)h * (32 * K) + 4 * m;
   float *x = S.buf + (size_t)tt * (size_t)S.token_stride + in_head;
   const float *wp;
   bool bias_in_w = false;
@@ -822,6 +829,7 @@ void launch_rmsnorm_rope(const RopeSide *sides, int n_sides, int n_tokens, int h
   a.n_heads01 = a.n_heads0 + (n_sides > 1 ? sides[1].n_heads : 0);
   a.heads_per_token = a.n_heads01 + (n_sides > 2 ? sides[2].n_heads : 0);
   a.n_heads = (unsigned)n_tokens * (unsigned)a.heads_per_token;
+  a.n_tokens = (unsigned)n_tokens;
   // heads per wave: 8 (8 lanes per head), 4 at head_dim 256 (16 lanes per head).  Where a side's
   // head count is not a multiple of that (up to head_dim 256), a large call takes the flat layout:
   // per group of 8 (4) tokens, n_heads waves for each side.  Its waves are full, but each lane
