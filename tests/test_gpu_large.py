@@ -264,10 +264,10 @@ def test_qkv_stage_with_caches_past_2_pow_32_elements(ops, oracle):
     assert same(host_rows(vc, pick).view(np.uint16), wvc)
 
 
-def test_kv_pack_kv_with_a_row_stride_past_2_pow_32(ops, oracle):
-    """The one-launch K/V pack with a source row stride of 2^32 + 4096 floats (two rows 17.2 GB apart): the
-    kernel form with 64-bit strides, which the launcher takes when a stride does not fit 32 bits."""
-    stride = (1 << 32) + 4096
+@pytest.mark.parametrize("stride", [(1 << 32) - 4, (1 << 32) + 4096])
+def test_kv_pack_kv_with_row_strides_around_2_pow_32(ops, oracle, stride):
+    """The one-launch K/V pack with a source row stride of 2^32 - 4 floats (the largest the 32-bit-stride kernel
+    form takes) and of 2^32 + 4096 (the 64-bit form): two rows 17.2 GB apart."""
     need(4 * (stride + 2048))
     g = gen(920)
     flat = torch.empty(stride + 2048, dtype=torch.float32, device="cuda")
